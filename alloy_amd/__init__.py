@@ -1,0 +1,20 @@
+"""alloy_amd — MI355X-native (gfx950) quantized-weight matmul.
+
+Drop-in for Alloy's quantized-linear path: GGUF Q8_0 / Q5_0 / Q4_K / Q6_K and
+MLX 4-bit affine weights, decode GEMV, prefill GEMM and routed-expert MoE, as
+hand-written HIP kernels behind a C ABI (``include/alloy_amd.h``) bound with
+ctypes.  Importing the package registers the ``torch.ops.alloy.*`` ops.
+"""
+
+from . import formats, synth
+from ._lib import LIB_PATH, LibraryMissing, lib
+from .modules import (GGUFQ4_KLinear, GGUFQ5_0Linear, GGUFQ6_KLinear, GGUFQ8_0Linear, GGUFQuantLinear,
+                      MLXMoeExperts, MLXQ4Linear)
+from .ops import dequant, mlx_moe_routed, moe_workspace_bytes, qmm, router_topk
+
+__all__ = [
+    "LIB_PATH", "LibraryMissing", "lib", "formats", "synth",
+    "GGUFQuantLinear", "GGUFQ8_0Linear", "GGUFQ5_0Linear", "GGUFQ4_KLinear", "GGUFQ6_KLinear",
+    "MLXQ4Linear", "MLXMoeExperts",
+    "qmm", "dequant", "router_topk", "mlx_moe_routed", "moe_workspace_bytes",
+]

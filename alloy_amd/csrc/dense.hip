@@ -1,0 +1,416 @@
+// Dense quantized matmul kernels for gfx950: dequant probe, M=1 GEMV (v_dot2),
+// M<=16 GEMV on MFMA, and the prefill GEMM on MFMA.  All launched on the caller's
+// HIP stream; no allocation, no global mutable state.
+#include "launch.h"
+
+namespace alloy {
+
+// ------------------------------------------------------------------ helpers
+template <typename XT>
+__device__ __forceinline__ f16x8 ld_x8(const XT* p);
+template <>
+__device__ __forceinline__ f16x8 ld_x8<f16>(const f16* p) { return *(const f16x8*)p; }
+template <>
+__device__ __forceinline__ f16x8 ld_x8<float>(const float* p) {
+  const f32x4 a = *(const f32x4*)p, b = *(const f32x4*)(p + 4);
+  f16x8 r;
+  r[0] = (f16)a[0]; r[1] = (f16)a[1]; r[2] = (f16)a[2]; r[3] = (f16)a[3];
+  r[4] = (f16)b[0]; r[5] = (f16)b[1]; r[6] = (f16)b[2]; r[7] = (f16)b[3];
+  return r;
+}
+
+__device__ __forceinline__ uint32_t pack2(f16 lo, f16 hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+}
+
+__device__ __forceinline__ void store_y(void* y, bool y_f32, int64_t i, float v) {
+  if (y_f32) ((float*)y)[i] = v;
+  else ((f16*)y)[i] = (f16)v;
+}
+
+template <class F>
+__device__ __forceinline__ void dec32_f16(const QArgs& a, int64_t n, int k0, f16x8 (&o)[4]) {
+  float w[32];
+  F::dec32(a, n, k0, w);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[j][e] = (f16)w[8 * j + e];   // RNE
+}
+
+// ------------------------------------------------------------------ dequant probe
+// One thread per (row, 32-element group).  out is [nrows, K] f32 (exact) or f16 (RN).
+template <class F>
+__global__ __launch_bounds__(256) void k_dequant(QArgs a, void* out, int out_f16, int64_t row0,
+                                                 int64_t nrows) {
+  const int64_t groups = a.K >> 5;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= nrows * groups) return;
+  const int64_t r = t / groups;
+  const int k0 = (int)(t - r * groups) * 32;
+  float w[32];
+  F::dec32(a, row0 + r, k0, w);
+  const int64_t o = r * a.K + k0;
+  if (out_f16) {
+    f16* p = (f16*)out + o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f16x8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (f16)w[8 * j + e];
+      *(f16x8*)(p + 8 * j) = v;
+    }
+  } else {
+    float* p = (float*)out + o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) *(f32x4*)(p + 4 * j) = f32x4{w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]};
+  }
+}
+
+// ------------------------------------------------------------------ M=1 GEMV (v_dot2)
+// x is staged once per workgroup into LDS as fp16 pairs in the format's XPERM order,
+// plus fp32 sums per 16 elements.  L lanes cooperate on one row (units strided by L),
+// so a wave covers 64/L rows per step; rows are grid-strided.  grid.y = x row.
+template <int XPERM, typename XT>
+__device__ __forceinline__ void stage_x(const XT* x, int K, uint32_t* xs, float* xs16) {
+  for (int g = threadIdx.x; g < (K >> 4); g += blockDim.x) {
+    f16x8 lo = ld_x8<XT>(x + 16 * g), hi = ld_x8<XT>(x + 16 * g + 8);
+    f16 v[16];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { v[e] = lo[e]; v[8 + e] = hi[e]; }
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s += (float)v[e];
+    uint32_t o[8];
+    if (XPERM == 4) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        o[2 * j] = pack2(v[4 * j], v[4 * j + 2]);
+        o[2 * j + 1] = pack2(v[4 * j + 1], v[4 * j + 3]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int b = 8 * j;
+        o[4 * j] = pack2(v[b], v[b + 4]);
+        o[4 * j + 1] = pack2(v[b + 2], v[b + 6]);
+        o[4 * j + 2] = pack2(v[b + 1], v[b + 5]);
+        o[4 * j + 3] = pack2(v[b + 3], v[b + 7]);
+      }
+    }
+    *(u32x4*)(xs + 8 * g) = u32x4{o[0], o[1], o[2], o[3]};
+    *(u32x4*)(xs + 8 * g + 4) = u32x4{o[4], o[5], o[6], o[7]};
+    xs16[g] = s;
+  }
+}
+
+template <class F, int L, typename XT>
+__global__ __launch_bounds__(256) void k_gemv_dot2(QArgs a, const XT* x, void* y, int y_f32,
+                                                   int64_t N) {
+  extern __shared__ uint32_t smem[];
+  const int K = a.K;
+  uint32_t* xs = smem;
+  float* xs16 = (float*)(smem + (K >> 1));
+  const int64_t m = blockIdx.y;
+  stage_x<F::XPERM, XT>(x + m * K, K, xs, xs16);
+  __syncthreads();
+
+  constexpr int RPW = 64 / L;
+  const int U = K / F::UE;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int sub = lane / L, li = lane % L;
+  const int64_t step = (int64_t)gridDim.x * 4 * RPW;
+  for (int64_t n0 = ((int64_t)blockIdx.x * 4 + wave) * RPW; n0 < N; n0 += step) {
+    const int64_t n = n0 + sub;
+    float acc = 0.f;
+    if (n < N) {
+#pragma unroll 4
+      for (int u = li; u < U; u += L) acc += F::unit_dot(a, n, u, xs, xs16);
+    }
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (li == 0 && n < N) store_y(y, y_f32, m * N + n, acc);
+  }
+}
+
+// ------------------------------------------------------------------ M<=16 GEMV on MFMA
+// v_mfma_f32_16x16x32_f16 with A = 16 weight rows (dequantised to fp16 in registers),
+// B = x^T (up to 16 activation rows).  A K-chunk of 128 elements is split over the
+// four 16-lane quarters (32 elements each, pieces of 8 per MFMA); the four waves of a
+// workgroup take chunks round-robin and are reduced through LDS in a fixed order.
+template <class F, int RG, typename XT>
+__global__ __launch_bounds__(256) void k_gemv_mfma(QArgs a, const XT* x, int M, void* y,
+                                                   int y_f32, int64_t N) {
+  __shared__ float red[3][RG][64][4];
+  const int K = a.K;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i = lane & 15, kq = lane >> 4;
+  const int64_t nb = (int64_t)blockIdx.x * 16 * RG;
+  const int mcol0 = blockIdx.y * 16;                     // x rows handled: mcol0 .. +16
+  const int mrow = mcol0 + i;
+  f32x4 acc[RG];
+#pragma unroll
+  for (int r = 0; r < RG; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int k0 = 128 * wave; k0 < K; k0 += 512) {
+    const int kk = k0 + 32 * kq;
+    const bool kin = kk < K;
+    f16x8 bfr[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (kin && mrow < M) bfr[j] = ld_x8<XT>(x + (int64_t)mrow * K + kk + 8 * j);
+      else bfr[j] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+      const int64_t n = nb + 16 * r + i;
+      f16x8 afr[4];
+      if (kin && n < N) dec32_f16<F>(a, n, kk, afr);
+      else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) afr[j] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afr[j], bfr[j], acc[r], 0, 0, 0);
+    }
+  }
+  // fixed-order cross-wave reduction: wave 0 adds waves 1, 2, 3 in order
+  if (wave > 0) {
+#pragma unroll
+    for (int r = 0; r < RG; ++r)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) red[wave - 1][r][lane][t] = acc[r][t];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+#pragma unroll
+      for (int w = 0; w < 3; ++w)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[r][t] += red[w][r][lane][t];
+      // D[row 4kq + t][col i]  ->  y[x row mcol0 + i][weight row nb + 16r + 4kq + t]
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int64_t n = nb + 16 * r + 4 * kq + t;
+        if (mrow < M && n < N) store_y(y, y_f32, (int64_t)mrow * N + n, acc[r][t]);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ prefill GEMM on MFMA
+// Tile 128 (x rows) x 128 (weight rows) x 64 (K), 4 waves as 2x2, each 64x64 from
+// 2x2 v_mfma_f32_32x32x16_f16.  The weight tile is dequantised (exact fp32 -> RN fp16)
+// straight into LDS; x is copied as fp16.
+constexpr int GBM = 128, GBN = 128, GBK = 64, GLD = GBK + 8;
+
+template <class F, typename XT>
+__global__ __launch_bounds__(256) void k_gemm(QArgs a, const XT* x, int M, void* y, int y_f32,
+                                              int64_t N) {
+  __shared__ f16 As[GBM][GLD];
+  __shared__ f16 Bs[GBN][GLD];
+  const int K = a.K;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = (int64_t)blockIdx.y * GBM;
+  const int64_t n0 = (int64_t)blockIdx.x * GBN;
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[tm][tn][e] = 0.f;
+
+  for (int k0 = 0; k0 < K; k0 += GBK) {
+    // x tile: 128 rows x 8 chunks of 8 halves
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int idx = tid + 256 * c, row = idx >> 3, col = (idx & 7) * 8;
+      const int64_t gm = m0 + row;
+      const int gk = k0 + col;
+      f16x8 v = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      if (gm < M && gk < K) v = ld_x8<XT>(x + gm * K + gk);
+      *(f16x8*)&As[row][col] = v;
+    }
+    // weight tile: 128 rows x 2 groups of 32
+    {
+      const int row = tid >> 1, kh = (tid & 1) * 32;
+      const int64_t gn = n0 + row;
+      f16x8 o[4];
+      if (gn < N && k0 + kh < K) dec32_f16<F>(a, gn, k0 + kh, o);
+      else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) *(f16x8*)&Bs[row][kh + 8 * j] = o[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < GBK; ks += 16) {
+      f16x8 af[2], bf[2];
+      const int kc = ks + 8 * (lane >> 5);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        af[t] = *(const f16x8*)&As[64 * wm + 32 * t + (lane & 31)][kc];
+        bf[t] = *(const f16x8*)&Bs[64 * wn + 32 * t + (lane & 31)][kc];
+      }
+#pragma unroll
+      for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn)
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[tm], bf[tn], acc[tm][tn], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  // D[i][j]: j = lane%32 (weight row), i = 8(t/4) + 4(lane/32) + t%4 (x row)
+#pragma unroll
+  for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn) {
+      const int64_t gn = n0 + 64 * wn + 32 * tn + (lane & 31);
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const int64_t gm = m0 + 64 * wm + 32 * tm + 8 * (t >> 2) + 4 * (lane >> 5) + (t & 3);
+        if (gm < M && gn < N) store_y(y, y_f32, gm * N + gn, acc[tm][tn][t]);
+      }
+    }
+}
+
+// ------------------------------------------------------------------ host launchers
+template <template <class> class Fn, typename... Args>
+static hipError_t by_fmt(int fmt, Args&&... args) {
+  switch (fmt) {
+    case F_Q8_0: return Fn<FQ80>::run(args...);
+    case F_Q5_0: return Fn<FQ50>::run(args...);
+    case F_Q4_K: return Fn<FQ4K>::run(args...);
+    case F_Q6_K: return Fn<FQ6K>::run(args...);
+    case F_MLX: return Fn<FMLX>::run(args...);
+    case F_Q8_0S: return Fn<FQ80S>::run(args...);
+    case F_Q5_0S: return Fn<FQ50S>::run(args...);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <class F>
+struct DequantRun {
+  static hipError_t run(const QArgs& a, void* out, bool out_f16, int64_t row0, int64_t nrows,
+                        hipStream_t st) {
+    const int64_t work = nrows * (a.K >> 5);
+    if (work == 0) return hipSuccess;
+    const int64_t blocks = (work + 255) / 256;
+    hipLaunchKernelGGL(k_dequant<F>, dim3((unsigned)blocks), dim3(256), 0, st, a, out,
+                       (int)out_f16, row0, nrows);
+    return hipGetLastError();
+  }
+};
+
+hipError_t launch_dequant(int fmt, const QArgs& a, void* out, bool out_f16, int64_t row0,
+                          int64_t nrows, hipStream_t st) {
+  return by_fmt<DequantRun>(fmt, a, out, out_f16, row0, nrows, st);
+}
+
+static int pow2_floor(int v) {
+  int p = 1;
+  while (p * 2 <= v) p *= 2;
+  return p;
+}
+
+template <class F>
+struct GemvDot2Run {
+  template <int L, typename XT>
+  static hipError_t go(const QArgs& a, const void* x, void* y, bool y_f32, int64_t M, int64_t N,
+                       int grid_cap, hipStream_t st) {
+    const size_t shm = (size_t)a.K * 2 + (size_t)(a.K / 16) * 4;
+    auto kfn = k_gemv_dot2<F, L, XT>;
+    if (shm > 65536) {
+      hipError_t e = hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+      if (e != hipSuccess) return e;
+    }
+    const int64_t rows_per_iter = 4 * (64 / L);
+    int64_t grid = (N + rows_per_iter - 1) / rows_per_iter;
+    const int64_t cap = grid_cap > 0 ? grid_cap : 2048;
+    if (grid > cap) grid = cap;
+    if (grid < 1) grid = 1;
+    hipLaunchKernelGGL(kfn, dim3((unsigned)grid, (unsigned)M), dim3(256), shm, st, a,
+                       (const XT*)x, y, (int)y_f32, N);
+    return hipGetLastError();
+  }
+  template <typename XT>
+  static hipError_t pick(int L, const QArgs& a, const void* x, void* y, bool y_f32, int64_t M,
+                         int64_t N, int cap, hipStream_t st) {
+    switch (L) {
+      case 4: return go<4, XT>(a, x, y, y_f32, M, N, cap, st);
+      case 8: return go<8, XT>(a, x, y, y_f32, M, N, cap, st);
+      case 16: return go<16, XT>(a, x, y, y_f32, M, N, cap, st);
+      case 32: return go<32, XT>(a, x, y, y_f32, M, N, cap, st);
+      default: return go<64, XT>(a, x, y, y_f32, M, N, cap, st);
+    }
+  }
+  static hipError_t run(const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32, int64_t M,
+                        int64_t N, const Opts& o, hipStream_t st) {
+    const int U = a.K / F::UE;
+    int L = o.lanes_per_row;
+    if (L <= 0) {
+      L = pow2_floor(U / 3 > 0 ? U / 3 : 1);
+      if (L < 4) L = 4;
+      if (L > 64) L = 64;
+    }
+    return x_f32 ? pick<float>(L, a, x, y, y_f32, M, N, o.grid_cap, st)
+                 : pick<f16>(L, a, x, y, y_f32, M, N, o.grid_cap, st);
+  }
+};
+
+hipError_t launch_gemv_dot2(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
+                            bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st) {
+  if (M == 0 || N == 0) return hipSuccess;
+  return by_fmt<GemvDot2Run>(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
+}
+
+template <class F>
+struct GemvMfmaRun {
+  template <int RG, typename XT>
+  static hipError_t go(const QArgs& a, const void* x, int M, void* y, bool y_f32, int64_t N,
+                       hipStream_t st) {
+    const int64_t grid = (N + 16 * RG - 1) / (16 * RG);
+    const int gy = (M + 15) / 16;
+    hipLaunchKernelGGL((k_gemv_mfma<F, RG, XT>), dim3((unsigned)grid, (unsigned)gy), dim3(256), 0, st,
+                       a, (const XT*)x, M, y, (int)y_f32, N);
+    return hipGetLastError();
+  }
+  static hipError_t run(const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32, int64_t M,
+                        int64_t N, const Opts& o, hipStream_t st) {
+    const int rg = o.row_groups == 2 ? 2 : 1;
+    if (x_f32) return rg == 2 ? go<2, float>(a, x, (int)M, y, y_f32, N, st) : go<1, float>(a, x, (int)M, y, y_f32, N, st);
+    return rg == 2 ? go<2, f16>(a, x, (int)M, y, y_f32, N, st) : go<1, f16>(a, x, (int)M, y, y_f32, N, st);
+  }
+};
+
+hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
+                            bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st) {
+  if (M == 0 || N == 0) return hipSuccess;
+  return by_fmt<GemvMfmaRun>(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
+}
+
+template <class F>
+struct GemmRun {
+  static hipError_t run(const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32, int64_t M,
+                        int64_t N, const Opts&, hipStream_t st) {
+    dim3 grid((unsigned)((N + GBN - 1) / GBN), (unsigned)((M + GBM - 1) / GBM));
+    if (x_f32)
+      hipLaunchKernelGGL((k_gemm<F, float>), grid, dim3(256), 0, st, a, (const float*)x, (int)M, y, (int)y_f32, N);
+    else
+      hipLaunchKernelGGL((k_gemm<F, f16>), grid, dim3(256), 0, st, a, (const f16*)x, (int)M, y, (int)y_f32, N);
+    return hipGetLastError();
+  }
+};
+
+hipError_t launch_gemm(int fmt, const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32,
+                       int64_t M, int64_t N, const Opts& o, hipStream_t st) {
+  if (M == 0 || N == 0) return hipSuccess;
+  return by_fmt<GemmRun>(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
+}
+
+}  // namespace alloy

@@ -1,0 +1,33 @@
+// Host-side launchers shared between the kernel translation units and the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "qformats.h"
+
+namespace alloy {
+
+enum Fmt : int { F_Q8_0 = 0, F_Q5_0 = 1, F_Q4_K = 2, F_Q6_K = 3, F_MLX = 4, F_Q8_0S = 5, F_Q5_0S = 6 };
+enum Path : int { P_AUTO = 0, P_GEMV = 1, P_GEMV_MFMA = 2, P_GEMM = 3 };
+
+// Launch-shape knobs (0 = automatic choice).
+struct Opts {
+  int lanes_per_row = 0;   // dot2 GEMV: lanes cooperating on one row (4..64)
+  int grid_cap = 0;        // dot2 GEMV: max workgroups (grid-stride beyond)
+  int row_groups = 0;      // MFMA GEMV: 16-row groups per workgroup (1, 2)
+};
+
+hipError_t launch_dequant(int fmt, const QArgs& a, void* out, bool out_f16, int64_t row0,
+                          int64_t nrows, hipStream_t st);
+hipError_t launch_gemv_dot2(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
+                            bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st);
+hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
+                            bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st);
+hipError_t launch_gemm(int fmt, const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32,
+                       int64_t M, int64_t N, const Opts& o, hipStream_t st);
+
+// dot2 GEMV stages x (K fp16 + K/16 fp32 sums) in LDS.
+constexpr int64_t kMaxKDot2 = 32768;
+
+}  // namespace alloy

@@ -1,0 +1,359 @@
+// Routed-expert MoE over MLX 4-bit experts for gfx950.
+//
+// Pipeline (all on the caller's stream, deterministic, no float atomics):
+//   1. k_router     per token: top-k logits (ties -> lowest index), softmax over k
+//                   (reference: packages/alloy-metal/src/alloy/std/moe.py:31-79)
+//   2. k_sort       one workgroup: stable counting sort of the T*k routes by expert
+//                   (order within an expert = route order), inverse permutation, and
+//                   a list of column tiles (<= 16 routes of one expert each)
+//                   (reference role: moe.py:504-735, without padding rows)
+//   3. k_gate_up    per (tile, 16 gate rows): gathered MFMA GEMV over the tile's
+//                   tokens, h = silu(G_e x) * (U_e x) stored fp16 per sorted route
+//                   (reference role: moe.py:82-135, 225-306; fused rows [0:I] gate,
+//                   [I:2I] up, packages/alloy-server/src/alloy_server/models/qwen3_5.py:383-385)
+//   4. k_down       per (tile, 16 hidden rows): D_e h -> fp32 partial per sorted route
+//   5. k_combine    y[t] = sum_s w[t,s] * partial[inv[t,s]] in slot order
+//                   (reference role: moe.py:479-501, fixed-order combine)
+// Each expert's weights are read once per column tile of its routed tokens.
+#include "moe.h"
+
+namespace alloy {
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+MoeLayout moe_layout(int64_t T, int E, int top_k, int64_t H, int64_t I) {
+  MoeLayout L;
+  L.R = T * top_k;
+  L.max_tiles = (L.R < E ? L.R : E) + (L.R + kMoeColTile - 1) / kMoeColTile;
+  size_t o = 0;
+  L.idx = o; o = align256(o + 4 * (size_t)L.R);
+  L.wts = o; o = align256(o + 4 * (size_t)L.R);
+  L.sorted = o; o = align256(o + 4 * (size_t)L.R);
+  L.inv = o; o = align256(o + 4 * (size_t)L.R);
+  L.tiles = o; o = align256(o + 16 * (size_t)L.max_tiles);
+  L.ntiles = o; o = align256(o + 4);
+  L.h = o; o = align256(o + 2 * (size_t)L.R * (size_t)I);
+  L.part = o; o = align256(o + 4 * (size_t)L.R * (size_t)H);
+  L.total = o;
+  return L;
+}
+
+// ------------------------------------------------------------------ router
+template <int VPL>
+__global__ __launch_bounds__(64) void k_router(const float* logits, int32_t* idx, float* wts, int E,
+                                               int top_k) {
+  __shared__ float sv[kMoeMaxTopK];
+  __shared__ int si[kMoeMaxTopK];
+  const int64_t t = blockIdx.x;
+  const int lane = threadIdx.x;
+  float v[VPL];
+  uint32_t used = 0;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int e = lane + 64 * j;
+    float f = -INFINITY;
+    if (e < E) {
+      f = logits[t * E + e];
+      if (f != f) f = -INFINITY;   // NaN never wins over a number
+    } else {
+      used |= 1u << j;
+    }
+    v[j] = f;
+  }
+  for (int k = 0; k < top_k; ++k) {
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int e = lane + 64 * j;
+      if (!((used >> j) & 1u) && (v[j] > bv || (v[j] == bv && e < bi))) { bv = v[j]; bi = e; }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if ((bi & 63) == lane) used |= 1u << (bi >> 6);
+    if (lane == 0) { sv[k] = bv; si[k] = bi; }
+  }
+  __syncthreads();
+  if (lane == 0) {
+    const float m0 = sv[0];
+    float sum = 0.f;
+    for (int k = 0; k < top_k; ++k) sum += expf(sv[k] - m0);
+    for (int k = 0; k < top_k; ++k) {
+      idx[t * top_k + k] = si[k];
+      wts[t * top_k + k] = expf(sv[k] - m0) / sum;
+    }
+  }
+}
+
+hipError_t launch_router(const float* logits, int32_t* idx, float* w, int64_t T, int E, int top_k,
+                         hipStream_t st) {
+  const int vpl = (E + 63) / 64;
+  dim3 g((unsigned)T), b(64);
+  if (vpl <= 2) hipLaunchKernelGGL(k_router<2>, g, b, 0, st, logits, idx, w, E, top_k);
+  else if (vpl <= 4) hipLaunchKernelGGL(k_router<4>, g, b, 0, st, logits, idx, w, E, top_k);
+  else if (vpl <= 8) hipLaunchKernelGGL(k_router<8>, g, b, 0, st, logits, idx, w, E, top_k);
+  else hipLaunchKernelGGL(k_router<16>, g, b, 0, st, logits, idx, w, E, top_k);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ sort
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(v, off, 64);
+    if (lane >= off) v += t;
+  }
+  return v;
+}
+
+// Exclusive scan of one value per thread over a 1024-thread block; returns the
+// exclusive prefix, *total gets the sum.  scratch: >= 16 ints of LDS.
+__device__ int block_excl_scan(int v, int* scratch, int* total) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int inc = wave_incl_scan(v, lane);
+  if (lane == 63) scratch[wave] = inc;
+  __syncthreads();
+  if (wave == 0) {
+    const int s = lane < 16 ? scratch[lane] : 0;
+    const int si = wave_incl_scan(s, lane);
+    if (lane < 16) scratch[16 + lane] = si - s;   // exclusive wave offsets
+    if (lane == 15) scratch[32] = si;
+  }
+  __syncthreads();
+  const int r = scratch[16 + wave] + inc - v;
+  *total = scratch[32];
+  __syncthreads();
+  return r;
+}
+
+constexpr int kSortWaves = 16;
+
+// dynamic LDS: wcnt[kSortWaves][E] ints + 64 ints scratch
+__global__ __launch_bounds__(1024) void k_sort(const int32_t* idx, int R, int E, int32_t* sorted,
+                                               int32_t* inv, int32_t* tiles, int32_t* ntiles) {
+  extern __shared__ int lds[];
+  int* wcnt = lds;                        // [w * E + e]
+  int* scratch = lds + kSortWaves * E;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  for (int i = tid; i < kSortWaves * E; i += 1024) wcnt[i] = 0;
+  __syncthreads();
+  const int per = (R + kSortWaves - 1) / kSortWaves;
+  const int r0 = wave * per < R ? wave * per : R;
+  const int r1 = r0 + per < R ? r0 + per : R;
+  for (int r = r0 + lane; r < r1; r += 64) atomicAdd(&wcnt[wave * E + idx[r]], 1);
+  __syncthreads();
+  int tot = 0;
+  if (tid < E)
+    for (int w = 0; w < kSortWaves; ++w) tot += wcnt[w * E + tid];
+  int all;
+  const int off = block_excl_scan(tid < E ? tot : 0, scratch, &all);
+  int ntot;
+  const int tb = block_excl_scan(tid < E ? (tot + kMoeColTile - 1) / kMoeColTile : 0, scratch, &ntot);
+  if (tid < E) {
+    int base = off;
+    for (int w = 0; w < kSortWaves; ++w) {
+      const int c = wcnt[w * E + tid];
+      wcnt[w * E + tid] = base;
+      base += c;
+    }
+  }
+  __syncthreads();
+  // stable placement: each wave walks its route range in order, 64 at a time
+  const uint64_t lt = (1ull << lane) - 1ull;
+  for (int c0 = r0; c0 < r1; c0 += 64) {
+    const int r = c0 + lane;
+    const bool valid = r < r1;
+    const int e = valid ? idx[r] : 0;
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 10; ++b) {
+      const bool bit = (e >> b) & 1;
+      const uint64_t bb = __ballot(valid && bit);
+      peers &= bit ? bb : ~bb;
+    }
+    if (valid) {
+      const int pos = wcnt[wave * E + e] + __popcll(peers & lt);
+      sorted[pos] = r;
+      inv[r] = pos;
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (valid && (peers >> lane) == 1ull) wcnt[wave * E + e] += __popcll(peers);
+    __builtin_amdgcn_wave_barrier();
+  }
+  if (tid < E) {
+    const int n = tot;
+    for (int j = 0; 16 * j < n; ++j) {
+      int32_t* tp = tiles + 4 * (tb + j);
+      tp[0] = tid;
+      tp[1] = off + 16 * j;
+      tp[2] = n - 16 * j < 16 ? n - 16 * j : 16;
+      tp[3] = 0;
+    }
+  }
+  if (tid == 0) *ntiles = ntot;
+}
+
+// ------------------------------------------------------------------ grouped GEMVs
+__device__ __forceinline__ void dec32_mlx_f16(const QArgs& a, int64_t n, int k0, f16x8 (&o)[4]) {
+  float w[32];
+  FMLX::dec32(a, n, k0, w);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[j][e] = (f16)w[8 * j + e];
+}
+
+// Fixed-order reduction of per-wave MFMA accumulators through LDS: wave 0 ends with
+// acc(w0) + acc(w1) + acc(w2) + acc(w3).
+template <int NA>
+__device__ __forceinline__ void reduce_waves(f32x4 (&acc)[NA], float (*red)[NA][64][4]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (wave > 0)
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) red[wave - 1][a][lane][t] = acc[a][t];
+  __syncthreads();
+  if (wave == 0)
+#pragma unroll
+    for (int w = 0; w < 3; ++w)
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[a][t] += red[w][a][lane][t];
+}
+
+__global__ __launch_bounds__(256) void k_gate_up(QArgs gu, const f16* x, const int32_t* sorted,
+                                                 const int32_t* tiles, const int32_t* ntiles,
+                                                 f16* h, int top_k, int I) {
+  __shared__ float red[3][2][64][4];
+  const int tile = blockIdx.x;
+  if (tile >= *ntiles) return;
+  const int e = tiles[4 * tile], p0 = tiles[4 * tile + 1], cnt = tiles[4 * tile + 2];
+  const int i0 = blockIdx.y * 16;
+  const int K = gu.K;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i = lane & 15, kq = lane >> 4;
+  const int64_t tok = i < cnt ? (int64_t)(sorted[p0 + i] / top_k) : -1;
+  const bool rin = i0 + i < I;
+  const int64_t rowg = (int64_t)e * 2 * I + i0 + i, rowu = rowg + I;
+  f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  for (int k0 = 128 * wave; k0 < K; k0 += 512) {
+    const int kk = k0 + 32 * kq;
+    const bool kin = kk < K;
+    f16x8 bfr[4], ag[4], au[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      bfr[j] = (kin && tok >= 0) ? *(const f16x8*)(x + tok * K + kk + 8 * j) : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    if (kin && rin) {
+      dec32_mlx_f16(gu, rowg, kk, ag);
+      dec32_mlx_f16(gu, rowu, kk, au);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ag[j] = au[j] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ag[j], bfr[j], acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(au[j], bfr[j], acc[1], 0, 0, 0);
+    }
+  }
+  reduce_waves<2>(acc, red);
+  if (wave == 0 && i < cnt) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int r = i0 + 4 * kq + t;
+      if (r < I) {
+        const float g = acc[0][t], u = acc[1][t];
+        h[(int64_t)(p0 + i) * I + r] = (f16)(g / (1.f + expf(-g)) * u);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_down(QArgs dn, const f16* h, const int32_t* tiles,
+                                              const int32_t* ntiles, float* part, int H) {
+  __shared__ float red[3][1][64][4];
+  const int tile = blockIdx.x;
+  if (tile >= *ntiles) return;
+  const int e = tiles[4 * tile], p0 = tiles[4 * tile + 1], cnt = tiles[4 * tile + 2];
+  const int j0 = blockIdx.y * 16;
+  const int K = dn.K;   // = I
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i = lane & 15, kq = lane >> 4;
+  const bool cin = i < cnt;
+  const bool rin = j0 + i < H;
+  const int64_t row = (int64_t)e * H + j0 + i;
+  f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
+  for (int k0 = 128 * wave; k0 < K; k0 += 512) {
+    const int kk = k0 + 32 * kq;
+    const bool kin = kk < K;
+    f16x8 bfr[4], af[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      bfr[j] = (kin && cin) ? *(const f16x8*)(h + (int64_t)(p0 + i) * K + kk + 8 * j) : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    if (kin && rin) dec32_mlx_f16(dn, row, kk, af);
+    else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) af[j] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[j], bfr[j], acc[0], 0, 0, 0);
+  }
+  reduce_waves<1>(acc, red);
+  if (wave == 0 && cin) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int r = j0 + 4 * kq + t;
+      if (r < H) part[(int64_t)(p0 + i) * H + r] = acc[0][t];
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_combine(const float* part, const int32_t* inv,
+                                                 const float* wts, float* y, int top_k, int H) {
+  const int64_t t = blockIdx.x;
+  const int j = blockIdx.y * 256 + threadIdx.x;
+  if (j >= H) return;
+  float acc = 0.f;
+  for (int s = 0; s < top_k; ++s) {
+    const int64_t r = t * top_k + s;
+    acc += wts[r] * part[(int64_t)inv[r] * H + j];
+  }
+  y[t * H + j] = acc;
+}
+
+hipError_t launch_mlx_moe(const MoeArgs& m, const MoeLayout& L, hipStream_t st) {
+  int32_t* idx = (int32_t*)(m.ws + L.idx);
+  float* wts = (float*)(m.ws + L.wts);
+  int32_t* sorted = (int32_t*)(m.ws + L.sorted);
+  int32_t* inv = (int32_t*)(m.ws + L.inv);
+  int32_t* tiles = (int32_t*)(m.ws + L.tiles);
+  int32_t* ntiles = (int32_t*)(m.ws + L.ntiles);
+  f16* h = (f16*)(m.ws + L.h);
+  float* part = (float*)(m.ws + L.part);
+  hipError_t e = launch_router(m.logits, idx, wts, m.T, m.E, m.top_k, st);
+  if (e != hipSuccess) return e;
+  const size_t shm = (size_t)(kSortWaves * m.E + 64) * sizeof(int);
+  if (shm > 65536) {
+    e = hipFuncSetAttribute((const void*)k_sort, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(k_sort, dim3(1), dim3(1024), shm, st, idx, (int)L.R, m.E, sorted, inv, tiles, ntiles);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(k_gate_up, dim3((unsigned)L.max_tiles, (unsigned)((m.I + 15) / 16)), dim3(256), 0, st,
+                     m.gu, m.x, sorted, tiles, ntiles, h, m.top_k, (int)m.I);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(k_down, dim3((unsigned)L.max_tiles, (unsigned)((m.H + 15) / 16)), dim3(256), 0, st,
+                     m.dn, h, tiles, ntiles, part, (int)m.H);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(k_combine, dim3((unsigned)m.T, (unsigned)((m.H + 255) / 256)), dim3(256), 0, st,
+                     part, inv, wts, m.y, m.top_k, (int)m.H);
+  return hipGetLastError();
+}
+
+}  // namespace alloy

@@ -1,0 +1,410 @@
+// Block decoders for the quantized-weight formats, written for gfx950 (wave64).
+//
+// Each format is a struct with three device entry points:
+//   dec32(a, n, k0, w[32])   exact fp32 weights of elements k0..k0+31 of row n
+//                            (k0 % 32 == 0); every product below is exact in fp32,
+//                            so Q8_0/Q5_0/Q6_K are exact and Q4_K/MLX are rounded
+//                            once — the values are bit-identical to the reference's
+//                            fp32 decode whatever the operation order.
+//   unit_dot(a, n, u, xs, xs16)
+//                            sum_e w_e * x_e over decode unit u of row n, for the
+//                            M=1 GEMV.  Quants are turned into fp16 "1 + q/2^b"
+//                            values by placing the b-bit quant in the top mantissa
+//                            bits of 0x3C00 (exact), dotted with x by v_dot2_f32_f16
+//                            (products exact, fp32 accumulation), and the 1.0 bias
+//                            is removed with the per-16-element x sums xs16.
+//                            xs holds x as fp16 pairs in the format's XPERM order.
+//   constants QK (block elements), UE (unit elements), XPERM (4 or 8).
+//
+// Layout citations (reference, read-only):
+//   Q8_0  packages/alloy-server/src/alloy_server/gguf/quant.py:497-521
+//   Q5_0  packages/alloy-server/src/alloy_server/gguf/quant.py:414-494
+//   Q4_K  tests/kernels/test_quant_q4k_native.py:45-70,
+//         packages/alloy-metal/src/alloy/std/quant.py:835-884
+//   Q6_K  packages/alloy-metal/src/alloy/std/quant.py:1200-1270
+//   MLX   packages/alloy-server/src/alloy_server/mlx/quant.py:1-24,
+//         packages/alloy-metal/src/alloy/std/quant.py:2486-2488
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Arguments describing one quantized weight matrix (N rows of K elements).
+struct QArgs {
+  const uint8_t* w;     // GGUF wire blocks | MLX qweight | split qweight
+  const uint8_t* aux;   // split Q5_0 qhigh
+  const uint16_t* s;    // fp16 bits: MLX scales | split scales
+  const uint16_t* b;    // fp16 bits: MLX biases
+  int64_t rb;           // bytes per row of w
+  int32_t gs;           // MLX group size
+  int32_t K;
+};
+
+__device__ __forceinline__ float h2f(uint32_t bits) {
+  return (float)__builtin_bit_cast(f16, (uint16_t)(bits & 0xFFFFu));
+}
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
+}
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*)p; }
+__device__ __forceinline__ uint32_t ldu16(const void* p) { return *(const uint16_t*)p; }
+
+// NW little-endian words starting at a 2-byte-aligned address p.  Reads only bytes
+// in [p - 2, p + 4*NW): aligned dword loads plus one u16 load, then v_alignbyte.
+template <int NW>
+__device__ __forceinline__ void ld_words_a2(const uint8_t* p, uint32_t (&o)[NW]) {
+  const uintptr_t a = (uintptr_t)p;
+  const uint32_t* q = (const uint32_t*)(a & ~(uintptr_t)3);
+  const uint32_t sh = (uint32_t)(a & 2);      // byte shift: 0 or 2
+  uint32_t t[NW + 1];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) t[i] = q[i];
+  t[NW] = ldu16(p + 4 * NW - 2);             // top half-word, in bounds either way
+#pragma unroll
+  for (int i = 0; i < NW; ++i) o[i] = __builtin_amdgcn_alignbyte(t[i + 1], t[i], sh);
+}
+
+// fp16 pair constants
+#define MAGIC1 0x3C003C00u   // fp16 1.0 in both halves
+
+// ------------------------------------------------------------------ Q4_K
+// 144 B: fp16 d | fp16 dmin | scales[12] | qs[128]; sub-block g (32 el) uses
+// get_scale_min_k4(g); element l of g is the low (g even) / high nibble of
+// qs[(g/2)*32 + l]; w = d*sc*q - dmin*m.
+__device__ __forceinline__ void q4k_scale_min(uint32_t S0, uint32_t S1, uint32_t S2, int g,
+                                              uint32_t& sc, uint32_t& m) {
+  if (g < 4) {
+    sc = (S0 >> (8 * g)) & 63u;
+    m = (S1 >> (8 * g)) & 63u;
+  } else {
+    const int j = 8 * (g - 4);
+    sc = ((S2 >> j) & 0xFu) | (((S0 >> (j + 6)) & 3u) << 4);
+    m = ((S2 >> (j + 4)) & 0xFu) | (((S1 >> (j + 6)) & 3u) << 4);
+  }
+}
+
+struct FQ4K {
+  static constexpr int QK = 256, BB = 144, UE = 64, XPERM = 4;
+
+  __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
+    const uint8_t* blk = a.w + n * a.rb + (int64_t)(k0 >> 8) * BB;
+    const int g = (k0 & 255) >> 5;
+    const u32x4 h = ld16(blk);
+    const float d = h2f(h.x), dmin = h2f(h.x >> 16);
+    uint32_t sc, m;
+    q4k_scale_min(h.y, h.z, h.w, g, sc, m);
+    const float dsc = d * (float)sc, dm = dmin * (float)m;
+    const uint8_t* qs = blk + 16 + 32 * (g >> 1);
+    const u32x4 q0 = ld16(qs), q1 = ld16(qs + 16);
+    const uint32_t words[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    const int sh = 4 * (g & 1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        w[4 * i + b] = dsc * (float)((words[i] >> (8 * b + sh)) & 15u) - dm;
+  }
+
+  // unit u = (superblock u/4, pair p = u%4): sub-blocks 2p (low nibbles) and 2p+1.
+  __device__ static float unit_dot(const QArgs& a, int64_t n, int u, const uint32_t* xs,
+                                   const float* xs16) {
+    const int p = u & 3;
+    const uint8_t* blk = a.w + n * a.rb + (int64_t)(u >> 2) * BB;
+    const u32x4 h = ld16(blk);
+    const u32x4 q0 = ld16(blk + 16 + 32 * p), q1 = ld16(blk + 32 + 32 * p);
+    const uint32_t words[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    const int e0 = 64 * u;                       // first element of the unit in the row
+    const uint32_t* xa = xs + (e0 >> 1);        // sub-block A pairs (perm4)
+    const uint32_t* xb = xa + 16;                // sub-block B pairs
+    float SA = 0.f, SB = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t v = words[i];
+      SA = dot2(((v << 6) & 0x03C003C0u) | MAGIC1, xa[2 * i], SA);
+      SA = dot2(((v >> 2) & 0x03C003C0u) | MAGIC1, xa[2 * i + 1], SA);
+      SB = dot2(((v << 2) & 0x03C003C0u) | MAGIC1, xb[2 * i], SB);
+      SB = dot2(((v >> 6) & 0x03C003C0u) | MAGIC1, xb[2 * i + 1], SB);
+    }
+    const float* xg = xs16 + (e0 >> 4);
+    const float XA = xg[0] + xg[1], XB = xg[2] + xg[3];
+    const float d16 = 16.f * h2f(h.x), dmin = h2f(h.x >> 16);
+    uint32_t scA, mA, scB, mB;
+    q4k_scale_min(h.y, h.z, h.w, 2 * p, scA, mA);
+    q4k_scale_min(h.y, h.z, h.w, 2 * p + 1, scB, mB);
+    const float cA = d16 * (float)scA, cB = d16 * (float)scB;
+    // sum(q x) = 16 (S - X);  w = d sc q - dmin m
+    return cA * SA - (cA + dmin * (float)mA) * XA + cB * SB - (cB + dmin * (float)mB) * XB;
+  }
+};
+
+// ------------------------------------------------------------------ Q6_K
+// 210 B: ql[128] | qh[64] | int8 scales[16] | fp16 d; element e = 128h+32s+l:
+// ql byte 64h+32(s&1)+l (nibble shift 4(s>>1)), qh byte 32h+l (shift 2s),
+// q = (nib | qh2<<4) - 32, scale 8h+2s+l/16; w = d*sc*q.
+struct FQ6K {
+  static constexpr int QK = 256, BB = 210, UE = 64, XPERM = 4;
+
+  __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
+    const uint8_t* blk = a.w + n * a.rb + (int64_t)(k0 >> 8) * BB;
+    const int e = k0 & 255, h = e >> 7, s = (e >> 5) & 3;
+    uint32_t ql[8], qh[8];
+    ld_words_a2<8>(blk + 64 * h + 32 * (s & 1), ql);
+    ld_words_a2<8>(blk + 128 + 32 * h, qh);
+    const uint32_t scp = ldu16(blk + 192 + 8 * h + 2 * s);
+    const float d = h2f(ldu16(blk + 208));
+    const float ds0 = d * (float)(int8_t)(scp & 0xFF), ds1 = d * (float)(int8_t)(scp >> 8);
+    const int nsh = 4 * (s >> 1), hsh = 2 * s;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int q = (int)(((ql[i] >> (8 * b + nsh)) & 15u) | (((qh[i] >> (8 * b + hsh)) & 3u) << 4)) - 32;
+        w[4 * i + b] = (i < 4 ? ds0 : ds1) * (float)q;
+      }
+  }
+
+  // unit u = (superblock u/4, half h = (u%4)/2, s0 = u%2): elements
+  // 128h+32*s0+l (low nibbles) and 128h+32*(s0+2)+l (high nibbles), l in [0,32).
+  __device__ static float unit_dot(const QArgs& a, int64_t n, int u, const uint32_t* xs,
+                                   const float* xs16) {
+    const int h = (u >> 1) & 1, s0 = u & 1;
+    const uint8_t* blk = a.w + n * a.rb + (int64_t)(u >> 2) * BB;
+    uint32_t ql[8], qh[8];
+    ld_words_a2<8>(blk + 64 * h + 32 * s0, ql);
+    ld_words_a2<8>(blk + 128 + 32 * h, qh);
+    const uint32_t scl = ldu16(blk + 192 + 8 * h + 2 * s0);       // scales (s0, l<16), (s0, l>=16)
+    const uint32_t sch = ldu16(blk + 192 + 8 * h + 2 * s0 + 4);   // scales (s0+2, ...)
+    const float d = h2f(ldu16(blk + 208));
+    const int eb = 256 * (u >> 2) + 128 * h;
+    const uint32_t* xlo = xs + ((eb + 32 * s0) >> 1);
+    const uint32_t* xhi = xs + ((eb + 32 * s0 + 64) >> 1);
+    const int c0 = 2 * s0;
+    float S[4] = {0.f, 0.f, 0.f, 0.f};   // (s0,l<16) (s0,l>=16) (s0+2,l<16) (s0+2,l>=16)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t v = ql[i], c = qh[i];
+      // 6-bit u in fp16 mantissa bits 4..9 -> value 1 + u/64
+      const uint32_t p0 = ((v << 4) & 0x00F000F0u) | ((c << (8 - c0)) & 0x03000300u) | MAGIC1;
+      const uint32_t p1 = ((v >> 4) & 0x00F000F0u) | ((c >> c0) & 0x03000300u) | MAGIC1;
+      const uint32_t p2 = (v & 0x00F000F0u) | ((c << (4 - c0)) & 0x03000300u) | MAGIC1;
+      const uint32_t p3 = ((v >> 8) & 0x00F000F0u) | ((c >> (c0 + 4)) & 0x03000300u) | MAGIC1;
+      const int r = i >> 2;
+      S[r] = dot2(p0, xlo[2 * i], S[r]);
+      S[r] = dot2(p1, xlo[2 * i + 1], S[r]);
+      S[2 + r] = dot2(p2, xhi[2 * i], S[2 + r]);
+      S[2 + r] = dot2(p3, xhi[2 * i + 1], S[2 + r]);
+    }
+    const float* xl = xs16 + ((eb + 32 * s0) >> 4);
+    const float* xh = xs16 + ((eb + 32 * s0 + 64) >> 4);
+    // sum((u-32) x) = 64 S - 96 X
+    float acc = (float)(int8_t)(scl & 0xFF) * (64.f * S[0] - 96.f * xl[0]);
+    acc += (float)(int8_t)(scl >> 8) * (64.f * S[1] - 96.f * xl[1]);
+    acc += (float)(int8_t)(sch & 0xFF) * (64.f * S[2] - 96.f * xh[0]);
+    acc += (float)(int8_t)(sch >> 8) * (64.f * S[3] - 96.f * xh[1]);
+    return d * acc;
+  }
+};
+
+// ------------------------------------------------------------------ Q8_0 (wire)
+// 34 B: fp16 d | int8 qs[32]; w = d*q.
+__device__ __forceinline__ float q8_words_dot(const uint32_t (&v)[8], const uint32_t* xp, float S) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t o = v[i] ^ 0x80808080u;       // offset binary u = q + 128
+    S = dot2(((o << 2) & 0x03FC03FCu) | MAGIC1, xp[2 * i], S);       // bytes 0,2 -> 1 + u/256
+    S = dot2(((o >> 6) & 0x03FC03FCu) | MAGIC1, xp[2 * i + 1], S);   // bytes 1,3
+  }
+  return S;
+}
+
+struct FQ80 {
+  static constexpr int QK = 32, BB = 34, UE = 32, XPERM = 4;
+
+  __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
+    const uint8_t* blk = a.w + n * a.rb + (int64_t)(k0 >> 5) * BB;
+    uint32_t v[8];
+    ld_words_a2<8>(blk + 2, v);
+    const float d = h2f(ldu16(blk));
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) w[4 * i + b] = d * (float)(int8_t)((v[i] >> (8 * b)) & 0xFF);
+  }
+
+  __device__ static float unit_dot(const QArgs& a, int64_t n, int u, const uint32_t* xs,
+                                   const float* xs16) {
+    const uint8_t* blk = a.w + n * a.rb + (int64_t)u * BB;
+    uint32_t v[8];
+    ld_words_a2<8>(blk + 2, v);
+    const float d = h2f(ldu16(blk));
+    const float S = q8_words_dot(v, xs + 16 * u, 0.f);
+    const float X = xs16[2 * u] + xs16[2 * u + 1];
+    return d * (256.f * S - 384.f * X);            // sum((u-128) x)
+  }
+};
+
+// Q8_0 split layout (reference loader): qweight int8[N,K], scales fp16[N,K/32].
+struct FQ80S {
+  static constexpr int QK = 32, BB = 32, UE = 32, XPERM = 4;
+
+  __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
+    const uint8_t* q = a.w + n * a.rb + k0;
+    const u32x4 q0 = ld16(q), q1 = ld16(q + 16);
+    const uint32_t v[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    const float d = h2f(a.s[n * (a.K >> 5) + (k0 >> 5)]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) w[4 * i + b] = d * (float)(int8_t)((v[i] >> (8 * b)) & 0xFF);
+  }
+
+  __device__ static float unit_dot(const QArgs& a, int64_t n, int u, const uint32_t* xs,
+                                   const float* xs16) {
+    const uint8_t* q = a.w + n * a.rb + 32 * u;
+    const u32x4 q0 = ld16(q), q1 = ld16(q + 16);
+    const uint32_t v[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    const float d = h2f(a.s[n * (a.K >> 5) + u]);
+    const float S = q8_words_dot(v, xs + 16 * u, 0.f);
+    const float X = xs16[2 * u] + xs16[2 * u + 1];
+    return d * (256.f * S - 384.f * X);
+  }
+};
+
+// ------------------------------------------------------------------ Q5_0 (wire)
+// 22 B: fp16 d | u32 qh | qs[16]; element l<16: (qs[l]&15) | bit_l(qh)<<4,
+// element l+16: (qs[l]>>4) | bit_{l+16}(qh)<<4; w = (q-16)*d.
+struct FQ50 {
+  static constexpr int QK = 32, BB = 22, UE = 32, XPERM = 4;
+
+  __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
+    const uint8_t* blk = a.w + n * a.rb + (int64_t)(k0 >> 5) * BB;
+    uint32_t qh1[1], qs[4];
+    ld_words_a2<1>(blk + 2, qh1);
+    ld_words_a2<4>(blk + 6, qs);
+    const uint32_t qh = qh1[0];
+    const float d = h2f(ldu16(blk));
+#pragma unroll
+    for (int l = 0; l < 16; ++l) {
+      const uint32_t byte = (qs[l >> 2] >> (8 * (l & 3))) & 0xFF;
+      const int lo = (int)((byte & 15u) | (((qh >> l) & 1u) << 4)) - 16;
+      const int hi = (int)((byte >> 4) | (((qh >> (l + 16)) & 1u) << 4)) - 16;
+      w[l] = d * (float)lo;
+      w[l + 16] = d * (float)hi;
+    }
+  }
+
+  __device__ static float unit_dot(const QArgs& a, int64_t n, int u, const uint32_t* xs,
+                                   const float* xs16) {
+    const uint8_t* blk = a.w + n * a.rb + (int64_t)u * BB;
+    uint32_t qh1[1], qs[4];
+    ld_words_a2<1>(blk + 2, qh1);
+    ld_words_a2<4>(blk + 6, qs);
+    const uint32_t qh = qh1[0];
+    const float d = h2f(ldu16(blk));
+    const uint32_t* xp = xs + 16 * u;
+    float S = 0.f;
+    // 5-bit u in fp16 mantissa bits 5..9 -> 1 + u/32; the 5th bits of elements
+    // (l, l+2) are spread to bits 9 and 25 by (t & 5) * 0x00800200.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t v = qs[i];
+      const int l = 4 * i;
+      const uint32_t hA0 = (((qh >> l) & 5u) * 0x00800200u) & 0x02000200u;
+      const uint32_t hA1 = (((qh >> (l + 1)) & 5u) * 0x00800200u) & 0x02000200u;
+      const uint32_t hB0 = (((qh >> (l + 16)) & 5u) * 0x00800200u) & 0x02000200u;
+      const uint32_t hB1 = (((qh >> (l + 17)) & 5u) * 0x00800200u) & 0x02000200u;
+      S = dot2(((v << 5) & 0x01E001E0u) | hA0 | MAGIC1, xp[2 * i], S);
+      S = dot2(((v >> 3) & 0x01E001E0u) | hA1 | MAGIC1, xp[2 * i + 1], S);
+      S = dot2(((v << 1) & 0x01E001E0u) | hB0 | MAGIC1, xp[8 + 2 * i], S);
+      S = dot2(((v >> 7) & 0x01E001E0u) | hB1 | MAGIC1, xp[8 + 2 * i + 1], S);
+    }
+    const float X = xs16[2 * u] + xs16[2 * u + 1];
+    return d * (32.f * S - 48.f * X);              // sum((u-16) x)
+  }
+};
+
+// Q5_0 split layout (reference loader): qweight u8[N,K/2] K-sequential nibbles,
+// qhigh u8[N,K/2] (5th bit of element k in bit 0 / of k+1 in bit 4 of byte k/2),
+// scales fp16[N,K/32].  packages/alloy-metal/src/alloy/std/quant.py:1025-1034.
+struct FQ50S {
+  static constexpr int QK = 32, BB = 16, UE = 32, XPERM = 8;
+
+  __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
+    const int64_t off = n * a.rb + (k0 >> 1);
+    const u32x4 q = ld16(a.w + off), hq = ld16(a.aux + off);
+    const uint32_t qv[4] = {q.x, q.y, q.z, q.w}, hv[4] = {hq.x, hq.y, hq.z, hq.w};
+    const float d = h2f(a.s[n * (a.K >> 5) + (k0 >> 5)]);
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      const int sh = 8 * ((e >> 1) & 3) + 4 * (e & 1);
+      const uint32_t nib = (qv[e >> 3] >> sh) & 15u, hb = (hv[e >> 3] >> sh) & 1u;
+      w[e] = d * (float)((int)(nib | (hb << 4)) - 16);
+    }
+  }
+
+  __device__ static float unit_dot(const QArgs& a, int64_t n, int u, const uint32_t* xs,
+                                   const float* xs16) {
+    const int64_t off = n * a.rb + 16 * u;
+    const u32x4 q = ld16(a.w + off), hq = ld16(a.aux + off);
+    const uint32_t qv[4] = {q.x, q.y, q.z, q.w}, hv[4] = {hq.x, hq.y, hq.z, hq.w};
+    const float d = h2f(a.s[n * (a.K >> 5) + u]);
+    const uint32_t* xp = xs + 16 * u;             // perm8 pairs
+    float S = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t v = qv[i], c = hv[i];
+      S = dot2(((v << 5) & 0x01E001E0u) | ((c << 9) & 0x02000200u) | MAGIC1, xp[4 * i], S);
+      S = dot2(((v >> 3) & 0x01E001E0u) | ((c << 1) & 0x02000200u) | MAGIC1, xp[4 * i + 1], S);
+      S = dot2(((v << 1) & 0x01E001E0u) | ((c << 5) & 0x02000200u) | MAGIC1, xp[4 * i + 2], S);
+      S = dot2(((v >> 7) & 0x01E001E0u) | ((c >> 3) & 0x02000200u) | MAGIC1, xp[4 * i + 3], S);
+    }
+    const float X = xs16[2 * u] + xs16[2 * u + 1];
+    return d * (32.f * S - 48.f * X);
+  }
+};
+
+// ------------------------------------------------------------------ MLX 4-bit affine
+// qweight u8[N,K/2]: byte k/2 low nibble = element k (even); scales/biases
+// fp16[N,K/gs]; w = s*q + b.  Units of 32 elements require gs % 32 == 0.
+struct FMLX {
+  static constexpr int QK = 32, BB = 16, UE = 32, XPERM = 8;
+
+  __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
+    const u32x4 q = ld16(a.w + n * a.rb + (k0 >> 1));
+    const uint32_t v[4] = {q.x, q.y, q.z, q.w};
+    const int64_t gi = n * (a.K / a.gs) + k0 / a.gs;
+    const float s = h2f(a.s[gi]), b = h2f(a.b[gi]);
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      const uint32_t nib = (v[e >> 3] >> (4 * (e & 7))) & 15u;
+      w[e] = s * (float)nib + b;
+    }
+  }
+
+  __device__ static float unit_dot(const QArgs& a, int64_t n, int u, const uint32_t* xs,
+                                   const float* xs16) {
+    const u32x4 q = ld16(a.w + n * a.rb + 16 * u);
+    const uint32_t v[4] = {q.x, q.y, q.z, q.w};
+    const int64_t gi = n * (a.K / a.gs) + (32 * u) / a.gs;
+    const float s = h2f(a.s[gi]), b = h2f(a.b[gi]);
+    const uint32_t* xp = xs + 16 * u;             // perm8 pairs
+    float S = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t v4 = v[i];
+      S = dot2(((v4 << 6) & 0x03C003C0u) | MAGIC1, xp[4 * i], S);       // (e0, e4)
+      S = dot2(((v4 >> 2) & 0x03C003C0u) | MAGIC1, xp[4 * i + 1], S);   // (e2, e6)
+      S = dot2(((v4 << 2) & 0x03C003C0u) | MAGIC1, xp[4 * i + 2], S);   // (e1, e5)
+      S = dot2(((v4 >> 6) & 0x03C003C0u) | MAGIC1, xp[4 * i + 3], S);   // (e3, e7)
+    }
+    const float X = xs16[2 * u] + xs16[2 * u + 1];
+    const float s16 = 16.f * s;
+    return s16 * S + (b - s16) * X;                // s sum(q x) + b X
+  }
+};

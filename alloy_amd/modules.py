@@ -1,0 +1,127 @@
+"""Drop-in quantized modules with the reference's buffer tables and forward.
+
+``GGUFQ{8_0,5_0,4_K,6_K}Linear`` mirror ``packages/alloy-server/src/alloy_server/gguf/quant.py:108-193``
+(same constructor keywords, buffer names/dtypes/shapes, validation errors and
+forward: flatten leading dims, call ``torch.ops.alloy.gguf_*_mm``, add the bias).
+``MLXQ4Linear`` mirrors ``packages/alloy-server/src/alloy_server/mlx/quant.py:27-59``.
+``MLXMoeExperts`` holds stacked MLX-4 experts with fused gate_up rows
+(``[0:I]`` gate, ``[I:2I]`` up, as ``models/qwen3_5.py:232-297`` fuses GGUF
+experts) and routes through ``torch.ops.alloy.mlx_moe_routed``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import ops as _ops  # noqa: F401  (registers torch.ops.alloy.*)
+from .formats import QUANT_FORMATS, QuantFormat, validate_mlx_buffers, validate_quant_buffers
+
+_MM = {
+    "q8_0": lambda: torch.ops.alloy.gguf_q8_0_mm.default,
+    "q5_0": lambda: torch.ops.alloy.gguf_q5_0_mm.default,
+    "q4_k": lambda: torch.ops.alloy.gguf_q4_k_mm.default,
+    "q6_k": lambda: torch.ops.alloy.gguf_q6_k_mm.default,
+}
+
+
+class GGUFQuantLinear(torch.nn.Module):
+    FORMAT: QuantFormat
+
+    def __init__(self, *, in_features: int, out_features: int, bias: torch.nn.Parameter | None = None,
+                 **buffers: torch.Tensor) -> None:
+        super().__init__()
+        validate_quant_buffers(self.FORMAT, buffers, rows=out_features, dim=in_features, kind="linear")
+        self.in_features = int(in_features)
+        self.out_features = int(out_features)
+        for b in self.FORMAT.buffers:
+            self.register_buffer(b.name, buffers[b.name].contiguous())
+        if bias is not None:
+            self.bias = bias
+        else:
+            self.register_parameter("bias", None)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x_shape = x.shape
+        flat = x.reshape(-1, self.in_features).contiguous()
+        out = _MM[self.FORMAT.name]()(flat, *(self._buffers[b.name] for b in self.FORMAT.buffers))
+        if self.bias is not None:
+            out = out + self.bias
+        return out.reshape(*x_shape[:-1], self.out_features)
+
+
+class GGUFQ8_0Linear(GGUFQuantLinear):
+    """Linear over the reference's split Q8_0 layout (int8 qweight + fp16 scales)."""
+    FORMAT = QUANT_FORMATS["q8_0"]
+
+
+class GGUFQ5_0Linear(GGUFQuantLinear):
+    """Linear over the reference's split Q5_0 layout (qweight, qhigh, scales)."""
+    FORMAT = QUANT_FORMATS["q5_0"]
+
+
+class GGUFQ4_KLinear(GGUFQuantLinear):
+    """Linear over GGUF-native Q4_K 144-byte superblocks."""
+    FORMAT = QUANT_FORMATS["q4_k"]
+
+
+class GGUFQ6_KLinear(GGUFQuantLinear):
+    """Linear over GGUF Q6_K 210-byte blocks."""
+    FORMAT = QUANT_FORMATS["q6_k"]
+
+
+class MLXQ4Linear(torch.nn.Module):
+    """Linear over MLX affine int4 groups: qweight (out, in//2) uint8, fp16 scales/biases."""
+
+    def __init__(self, *, in_features: int, out_features: int, qweight: torch.Tensor, scales: torch.Tensor,
+                 biases: torch.Tensor, bias: torch.nn.Parameter | None = None) -> None:
+        super().__init__()
+        validate_mlx_buffers(qweight, scales, biases, rows=out_features, dim=in_features, kind="linear")
+        self.in_features = int(in_features)
+        self.out_features = int(out_features)
+        self.register_buffer("qweight", qweight.contiguous())
+        self.register_buffer("scales", scales.contiguous())
+        self.register_buffer("biases", biases.contiguous())
+        if bias is not None:
+            self.bias = bias
+        else:
+            self.register_parameter("bias", None)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x_shape = x.shape
+        flat = x.reshape(-1, self.in_features).contiguous()
+        out = torch.ops.alloy.mlx_q4_mm.default(flat, self.qweight, self.scales, self.biases)
+        if self.bias is not None:
+            out = out + self.bias
+        return out.reshape(*x_shape[:-1], self.out_features)
+
+
+class MLXMoeExperts(torch.nn.Module):
+    """Stacked MLX-4 routed experts: gate_up (E, 2I, H/2) + down (E, H, I/2).
+
+    ``forward(hidden (T,H) f16, router_logits (T,E) f32) -> (T,H) f32`` — top-k
+    routing, softmax over the k winners, ``sum_s w_s * down_e(silu(gate_e x) * up_e x)``.
+    """
+
+    def __init__(self, *, num_experts: int, top_k: int, hidden_size: int, moe_intermediate: int,
+                 gate_up_qweight, gate_up_scales, gate_up_biases, down_qweight, down_scales, down_biases):
+        super().__init__()
+        self.num_experts, self.top_k = int(num_experts), int(top_k)
+        self.hidden_size, self.moe_intermediate = int(hidden_size), int(moe_intermediate)
+        E, I, H = self.num_experts, self.moe_intermediate, self.hidden_size
+        validate_mlx_buffers(gate_up_qweight.reshape(E * 2 * I, -1), gate_up_scales.reshape(E * 2 * I, -1),
+                             gate_up_biases.reshape(E * 2 * I, -1), rows=E * 2 * I, dim=H, kind="moe gate_up")
+        validate_mlx_buffers(down_qweight.reshape(E * H, -1), down_scales.reshape(E * H, -1),
+                             down_biases.reshape(E * H, -1), rows=E * H, dim=I, kind="moe down")
+        for name, t in (("gate_up_qweight", gate_up_qweight), ("gate_up_scales", gate_up_scales),
+                        ("gate_up_biases", gate_up_biases), ("down_qweight", down_qweight),
+                        ("down_scales", down_scales), ("down_biases", down_biases)):
+            self.register_buffer(name, t.contiguous())
+
+    def forward(self, hidden: torch.Tensor, router_logits: torch.Tensor) -> torch.Tensor:
+        shape = hidden.shape
+        flat = hidden.reshape(-1, self.hidden_size).contiguous()
+        logits = router_logits.reshape(-1, self.num_experts).to(torch.float32).contiguous()
+        y = torch.ops.alloy.mlx_moe_routed.default(
+            flat, logits, self.gate_up_qweight, self.gate_up_scales, self.gate_up_biases, self.down_qweight,
+            self.down_scales, self.down_biases, self.num_experts, self.top_k, self.moe_intermediate)
+        return y.reshape(*shape[:-1], self.hidden_size)

@@ -1,0 +1,255 @@
+"""Benchmark: Q4_K decode GEMV weight GB/s on one MI355X, plus the prefill GEMM.
+
+Default workload (the config the headline metric is quoted on): one decode step
+of Llama-3.2-3B's Q4_K linear layers at M=1 — 28 layers x (q, k, v, o, gate, up,
+down) + lm_head = 197 GEMVs over 1,807,073,280 weight bytes (synthetic weights with
+the benchmark distribution, fp16 N(0,1) activations, fp32 output).  The weight set
+is 7x the 256 MB Infinity Cache, so every launch streams its weights from HBM.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--suite PATH]
+
+Prints ONE JSON line.  ``value`` = total weight bytes x K / elapsed time of the K
+timed steps (HIP events on the launch stream, synchronized on both sides).
+``roofline`` is for the dominant kernel (the Q4_K v_dot2 GEMV), from per-launch
+HIP event pairs in a separate instrumented pass of the same step.  ``cpu_baseline``
+times the CPU oracle (NumPy dequant + PyTorch-CPU fp32 matmul) on one layer.
+``prefill_gemm`` reports the Q4_K MFMA GEMM at M=2048 on the three config-4 shapes.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2516.6
+
+LAYERS = 28
+# (name, K, N) per transformer layer, then lm_head
+LLAMA32_3B = [("q", 3072, 3072), ("k", 3072, 1024), ("v", 3072, 1024), ("o", 3072, 3072),
+              ("gate", 3072, 8192), ("up", 3072, 8192), ("down", 8192, 3072)]
+LM_HEAD = ("lm_head", 3072, 128256)
+PREFILL = [(4096, 4096), (4096, 14336), (14336, 4096)]   # (K, N)
+
+
+def q4k_bytes(K, N):
+    return (K // 256) * 144 * N
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def build_decode_step(dev):
+    import torch
+    from alloy_amd import synth
+
+    mats = []
+    seed = 1000
+    for layer in range(LAYERS):
+        for name, K, N in LLAMA32_3B:
+            mats.append((f"{name}{layer}", K, N, synth.torch_blocks("q4_k", N, K, seed, dev)))
+            seed += 1
+    name, K, N = LM_HEAD
+    mats.append((name, K, N, synth.torch_blocks("q4_k", N, K, seed, dev)))
+    xs = {K: synth.torch_x(1, K, 7 + K, dev) for K in (3072, 8192)}
+    ys = {N: torch.empty((1, N), dtype=torch.float32, device=dev) for N in {m[2] for m in mats}}
+    return mats, xs, ys
+
+
+def run_step(mats, xs, ys, qmm):
+    for _, K, N, w in mats:
+        qmm("q4_k", xs[K], w, out=ys[N])
+
+
+def time_steps(fn, steps, warmup, stream):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1000.0
+
+
+def per_launch_times(mats, xs, ys, qmm, stream, reps=3):
+    """Instrumented pass: an event before and after every launch (same stream)."""
+    import torch
+
+    per = {}
+    for _ in range(reps):
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(len(mats) + 1)]
+        evs[0].record(stream)
+        for i, (_, K, N, w) in enumerate(mats):
+            qmm("q4_k", xs[K], w, out=ys[N])
+            evs[i + 1].record(stream)
+        torch.cuda.synchronize()
+        for i, (name, K, N, _) in enumerate(mats):
+            per.setdefault((K, N), []).append(evs[i].elapsed_time(evs[i + 1]) / 1000.0)
+    return per
+
+
+def cpu_baseline(seconds_target=15.0):
+    """CPU oracle on one transformer layer's 7 matrices: NumPy dequant + torch fp32 matmul."""
+    import numpy as np
+    import torch
+
+    from alloy_amd import synth
+    from oracle import quant as oq
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    rng = np.random.default_rng(0)
+    layer = [(K, N, synth.numpy_blocks("q4_k", N, K, rng)) for _, K, N in LLAMA32_3B]
+    xs = {K: torch.from_numpy(synth.numpy_x(1, K, rng)).float() for K in (3072, 8192)}
+    nbytes = sum(q4k_bytes(K, N) for K, N, _ in layer)
+
+    def one():
+        for K, N, blob in layer:
+            W = torch.from_numpy(oq.dequant_q4_k(blob, K))
+            torch.matmul(xs[K], W.T)
+
+    one()   # warm-up
+    times = []
+    t_all = time.perf_counter()
+    while time.perf_counter() - t_all < seconds_target or len(times) < 3:
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 50:
+            break
+    med = sorted(times)[len(times) // 2]
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(nbytes / med / 1e9, 4),
+        "unit": "weight GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"one Llama-3.2-3B layer (7 Q4_K matrices, {nbytes} weight bytes), M=1, "
+                  f"NumPy dequant + torch fp32 matmul per call, median of {len(times)} reps",
+        "ms_per_call": round(med * 1e3, 2),
+        "cpu_model": model,
+        "os_cpu_count": os.cpu_count(),
+    }
+
+
+def prefill_gemm(dev, qmm, M=2048, reps=5):
+    import torch
+
+    from alloy_amd import synth
+
+    out = []
+    for K, N in PREFILL:
+        w = synth.torch_blocks("q4_k", N, K, 77 + N, dev)
+        x = synth.torch_x(M, K, 78 + K, dev)
+        y = torch.empty((M, N), dtype=torch.float32, device=dev)
+        stream = torch.cuda.current_stream(dev)
+        t = time_steps(lambda: qmm("q4_k", x, w, out=y, path="gemm"), reps, 2, stream) / reps
+        tf = 2.0 * M * N * K / t / 1e12
+        out.append({"M": M, "K": K, "N": N, "us": round(t * 1e6, 1), "tflops": round(tf, 2),
+                    "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)})
+        del w, x, y
+    return out
+
+
+def traffic_from_profiles():
+    """HBM bytes per launch of the dominant kernel, from the committed PMC summary."""
+    p = ROOT / "profiles" / "q4k_gemv_decode_pmc.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import alloy_amd
+    from alloy_amd import qmm
+
+    dev = torch.device("cuda:0")
+    alloy_amd.lib()
+    log("building decode step weights ...")
+    mats, xs, ys = build_decode_step(dev)
+    total_bytes = sum(q4k_bytes(K, N) for _, K, N, _ in mats)
+    stream = torch.cuda.current_stream(dev)
+    log(f"{len(mats)} GEMVs, {total_bytes} weight bytes; timing {args.steps} steps")
+    t = time_steps(lambda: run_step(mats, xs, ys, qmm), args.steps, args.warmup, stream)
+    ms = t / args.steps * 1e3
+    value = total_bytes * args.steps / t / 1e9
+
+    per = per_launch_times(mats, xs, ys, qmm, stream)
+    tot_t = sum(sum(v) / len(v) * sum(1 for m in mats if (m[1], m[2]) == key) for key, v in per.items())
+    achieved = total_bytes / tot_t / 1e9
+    launches = len(mats)
+    shapes = {f"{K}x{N}": {"us": round(sum(v) / len(v) * 1e6, 2),
+                           "GBps": round(q4k_bytes(K, N) / (sum(v) / len(v)) / 1e9, 1)}
+              for (K, N), v in per.items()}
+    log(json.dumps(shapes))
+
+    prefill = None if args.no_prefill else prefill_gemm(dev, qmm)
+    if prefill:
+        log(json.dumps(prefill))
+    cpu = None if args.no_cpu else cpu_baseline()
+
+    rec = {
+        "metric": "Q4_K decode GEMV weight GB/s (% HBM peak); Q4_K prefill GEMM TFLOP/s",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k weights x fp16 activations, fp32 accumulate",
+        "data": "synthetic (BASELINE config 2 distributions), weights resident in HBM",
+        "config": {"workload": "Llama-3.2-3B Q4_K decode step, M=1: 28 layers x (q,k,v,o,gate,up,down) + lm_head",
+                   "launches_per_step": launches, "weight_bytes_per_step": total_bytes,
+                   "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
+                     "kernel": "k_gemv_dot2<FQ4K> (Q4_K M=1 GEMV)",
+                     "bytes_per_launch": round(total_bytes / launches),
+                     "avg_launch_us": round(tot_t / launches * 1e6, 3), "per_shape": shapes},
+        "cpu_baseline": cpu,
+        "prefill_gemm": prefill,
+    }
+    print(json.dumps(rec))
+
+
+if __name__ == "__main__":
+    main()

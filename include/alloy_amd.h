@@ -1,0 +1,172 @@
+/*
+ * alloy_amd — C ABI of the MI355X (gfx950) quantized-weight matmul library.
+ *
+ * Drop-in boundary for Alloy's quantized-linear operator surface.  Each named
+ * entry point replaces one `torch.ops.alloy.*` custom op of the reference
+ * (schemas at packages/alloy-torch/src/alloy_torch/custom_ops.py, cited per
+ * function below); the Python package binds these through ctypes and registers
+ * the same op names.
+ *
+ * Conventions
+ *   - Every pointer is a DEVICE pointer owned by the caller; the library never
+ *     allocates memory and never keeps state between calls.
+ *   - `stream` is a hipStream_t (NULL = default stream); all work is enqueued on
+ *     it, asynchronously.  Calls are reentrant; concurrent calls on different
+ *     streams do not interact.
+ *   - Outputs are fully overwritten (no pre-zeroing needed).  Results are
+ *     deterministic: no floating-point atomics anywhere.
+ *   - Row-major everywhere: activations x[M,K], output y[M,N], weight row n
+ *     holds K elements.  Weight buffers must be 16-byte aligned.
+ *   - On failure a status != ALLOY_OK is returned and alloy_last_error() holds a
+ *     thread-local message.  Status -> Python exception mapping mirrors the
+ *     reference's validation (packages/alloy-server/src/alloy_server/gguf/quant.py:81-105,
+ *     230-249; packages/alloy-server/src/alloy_server/mlx/quant.py:88-109).
+ */
+#ifndef ALLOY_AMD_H
+#define ALLOY_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  ALLOY_OK = 0,
+  ALLOY_E_SHAPE = 1,       /* ValueError: shape / divisibility */
+  ALLOY_E_DTYPE = 2,       /* TypeError: unsupported dtype code */
+  ALLOY_E_ALIGN = 3,       /* ValueError: pointer alignment */
+  ALLOY_E_UNSUPPORTED = 4, /* NotImplementedError: unsupported format / size */
+  ALLOY_E_HIP = 5,         /* RuntimeError: HIP launch / runtime failure */
+  ALLOY_E_ARG = 6          /* ValueError: bad argument (null pointer, bad enum) */
+} alloy_status;
+
+typedef enum {
+  ALLOY_FMT_Q8_0 = 0,      /* GGUF wire blocks, 34 B / 32 weights */
+  ALLOY_FMT_Q5_0 = 1,      /* GGUF wire blocks, 22 B / 32 weights */
+  ALLOY_FMT_Q4_K = 2,      /* GGUF wire blocks, 144 B / 256 weights */
+  ALLOY_FMT_Q6_K = 3,      /* GGUF wire blocks, 210 B / 256 weights */
+  ALLOY_FMT_MLX_Q4 = 4,    /* MLX affine 4-bit: qweight u8[N,K/2], fp16 scales/biases [N,K/gs] */
+  ALLOY_FMT_Q8_0_SPLIT = 5,/* reference loader layout: int8 qweight[N,K] + fp16 scales[N,K/32] */
+  ALLOY_FMT_Q5_0_SPLIT = 6 /* reference loader layout: u8 qweight[N,K/2] + u8 qhigh[N,K/2] + fp16 scales[N,K/32] */
+} alloy_format;
+
+typedef enum { ALLOY_DT_F32 = 0, ALLOY_DT_F16 = 1 } alloy_dtype;
+
+typedef enum {
+  ALLOY_PATH_AUTO = 0,      /* M==1 -> GEMV (v_dot2); M<=16 -> MFMA GEMV; else MFMA GEMM */
+  ALLOY_PATH_GEMV = 1,      /* v_dot2 GEMV, one x row per grid row (any M) */
+  ALLOY_PATH_GEMV_MFMA = 2, /* MFMA GEMV, 16 x rows per column tile (any M) */
+  ALLOY_PATH_GEMM = 3       /* MFMA GEMM with fp16-in-LDS dequant (any M) */
+} alloy_path;
+
+/*
+ * Generic quantized matmul: y[M,N] = x[M,K] @ dequant(w)[N,K]^T.
+ *   w, scales, biases, aux: the format's buffers (unused ones may be NULL):
+ *     GGUF wire formats: w = blocks[N, K/QK*block_bytes]
+ *     MLX_Q4:            w = qweight, scales, biases, group_size
+ *     Q8_0_SPLIT:        w = qweight (int8), scales
+ *     Q5_0_SPLIT:        w = qweight, aux = qhigh, scales
+ *   `opts` packs launch knobs for tuning (0 = automatic): bits 0-7 lanes per
+ *   row of the v_dot2 GEMV, bits 8-23 its grid cap, bits 24-27 MFMA GEMV row groups.
+ * No reference counterpart as a single op: the reference dispatches per format
+ * (packages/alloy-torch/src/alloy_torch/ops/linalg.py:346-739); the named entry
+ * points below are the per-op replacements and all route here.
+ */
+alloy_status alloy_qmm(alloy_format fmt, const void* w, const void* aux, const void* scales,
+                       const void* biases, int32_t group_size, const void* x, alloy_dtype x_dtype,
+                       void* y, alloy_dtype y_dtype, int64_t M, int64_t N, int64_t K,
+                       alloy_path path, int64_t opts, void* stream);
+
+/* torch.ops.alloy.gguf_q4_k_mm(activations, blocks) — custom_ops.py:47-49 */
+alloy_status alloy_gguf_q4_k_mm(const void* x, alloy_dtype x_dtype, const void* blocks, void* y,
+                                alloy_dtype y_dtype, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* torch.ops.alloy.gguf_q6_k_mm(activations, packed_weights) — custom_ops.py:96 */
+alloy_status alloy_gguf_q6_k_mm(const void* x, alloy_dtype x_dtype, const void* packed_weights,
+                                void* y, alloy_dtype y_dtype, int64_t M, int64_t N, int64_t K,
+                                void* stream);
+
+/* torch.ops.alloy.gguf_q8_0_mm(activations, qweight, scales) — custom_ops.py:104
+ * (the reference's split layout: int8 qweight[N,K], fp16 scales[N,K/32]) */
+alloy_status alloy_gguf_q8_0_mm(const void* x, alloy_dtype x_dtype, const void* qweight,
+                                const void* scales, void* y, alloy_dtype y_dtype, int64_t M,
+                                int64_t N, int64_t K, void* stream);
+
+/* torch.ops.alloy.gguf_q5_0_mm(activations, qweight, qhigh, scales) — custom_ops.py:86-88
+ * (the reference's split layout, packages/alloy-server/src/alloy_server/gguf/quant.py:414-494) */
+alloy_status alloy_gguf_q5_0_mm(const void* x, alloy_dtype x_dtype, const void* qweight,
+                                const void* qhigh, const void* scales, void* y,
+                                alloy_dtype y_dtype, int64_t M, int64_t N, int64_t K,
+                                void* stream);
+
+/* Raw GGUF wire-block Q8_0 / Q5_0 (the blob as stored in a .gguf file).  The
+ * reference repacks these at load (gguf/quant.py:414-521); these read the blob
+ * directly.  Same math as alloy_gguf_q8_0_mm / alloy_gguf_q5_0_mm. */
+alloy_status alloy_gguf_q8_0_blocks_mm(const void* x, alloy_dtype x_dtype, const void* blocks,
+                                       void* y, alloy_dtype y_dtype, int64_t M, int64_t N,
+                                       int64_t K, void* stream);
+alloy_status alloy_gguf_q5_0_blocks_mm(const void* x, alloy_dtype x_dtype, const void* blocks,
+                                       void* y, alloy_dtype y_dtype, int64_t M, int64_t N,
+                                       int64_t K, void* stream);
+
+/* torch.ops.alloy.mlx_q4_mm(activations, qweight, scales, biases) — custom_ops.py:72-74.
+ * group_size = 2*qweight_cols / scales_cols (packages/alloy-torch/src/alloy_torch/ops/linalg.py:509-511);
+ * this build requires group_size % 32 == 0. */
+alloy_status alloy_mlx_q4_mm(const void* x, alloy_dtype x_dtype, const void* qweight,
+                             const void* scales, const void* biases, int32_t group_size, void* y,
+                             alloy_dtype y_dtype, int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
+ * Dequantisation probe: rows [row0, row0+nrows) of the weight decoded to
+ * out[nrows, K] as fp32 (out_dtype F32: exact values, bit-identical to the
+ * reference decode) or fp16 (F16: round-to-nearest-even of those values — the
+ * operand the MFMA paths feed).  Replaces the decode half of the reference's
+ * embedding ops (custom_ops.py:67-69, 83-85, 89-91, 97-99, 103; quant.py:811-884, 1165-1270, 2804-2830).
+ */
+alloy_status alloy_dequant(alloy_format fmt, const void* w, const void* aux, const void* scales,
+                           const void* biases, int32_t group_size, void* out,
+                           alloy_dtype out_dtype, int64_t row0, int64_t nrows, int64_t N,
+                           int64_t K, void* stream);
+
+/*
+ * MoE router — moe_router_topk (packages/alloy-metal/src/alloy/std/moe.py:31-79):
+ * per token the top_k largest logits (descending, ties to the lowest index) and a
+ * softmax over those k.  logits f32[T,E] -> idx i32[T,top_k], weights f32[T,top_k].
+ */
+alloy_status alloy_moe_router_topk(const float* logits, int32_t* idx, float* weights, int64_t T,
+                                   int32_t E, int32_t top_k, void* stream);
+
+/* Workspace bytes alloy_mlx_moe_routed needs for (T, E, top_k, H, I). */
+size_t alloy_moe_workspace_bytes(int64_t T, int32_t E, int32_t top_k, int64_t H, int64_t I);
+
+/*
+ * Routed-expert MoE block over MLX 4-bit experts — the MLX-weight counterpart of
+ * torch.ops.alloy.gguf_moe_routed (custom_ops.py:63-66; handler
+ * packages/alloy-torch/src/alloy_torch/ops/moe.py:110-249):
+ *   router top-k -> per routed (token, slot): h = silu(G_e x) * (U_e x)
+ *   -> y[t] = sum_s w[t,s] * (D_e h), summed in slot order.
+ *   hidden f16[T,H]; router_logits f32[T,E]
+ *   gate_up: qweight u8[E, 2I, H/2] (rows [0:I] gate, [I:2I] up), scales/biases f16[E, 2I, H/gs]
+ *   down:    qweight u8[E, H, I/2],  scales/biases f16[E, H, I/gs]
+ *   y f32[T,H].  workspace: >= alloy_moe_workspace_bytes(...) bytes, 256-B aligned.
+ */
+alloy_status alloy_mlx_moe_routed(const void* hidden, const float* router_logits,
+                                  const void* gu_qweight, const void* gu_scales,
+                                  const void* gu_biases, const void* dn_qweight,
+                                  const void* dn_scales, const void* dn_biases,
+                                  int32_t group_size, int32_t E, int32_t top_k, int64_t T,
+                                  int64_t H, int64_t I, void* workspace, size_t workspace_bytes,
+                                  float* y, void* stream);
+
+/* Thread-local message of the last failed call on this thread ("" if none). */
+const char* alloy_last_error(void);
+/* Library version string. */
+const char* alloy_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ALLOY_AMD_H */

@@ -1,0 +1,185 @@
+"""GPU parity of the dense path (dequant probe, v_dot2 GEMV, MFMA GEMV, MFMA GEMM)
+against the NumPy oracle, through the C ABI.
+
+Bars (from the north star): dequantised fp32 weights bit-exact; fp16 staging values
+equal to RN16 of them; matmul relative Frobenius error <= 1e-3 and per-element
+|err| <= 2e-3 * ||x_m|| * max|w_n|.  Full benchmark shapes are checked on sampled
+weight rows (the oracle decodes only those rows)."""
+
+import numpy as np
+import pytest
+import torch
+
+import alloy_amd
+from alloy_amd import synth
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+
+FORMATS = ["q8_0", "q5_0", "q4_k", "q6_k", "mlx_q4", "q8_0_split", "q5_0_split"]
+REL_FRO, MAX_RATIO = 1e-3, 2e-3
+
+
+class Weight:
+    """A synthetic weight in one format: device buffers + oracle fp32 values."""
+
+    def __init__(self, fmt, N, K, rng, dev, gs=64):
+        self.fmt, self.N, self.K, self.gs = fmt, N, K, 0
+        self.scales = self.biases = self.aux = None
+        base = fmt.replace("_split", "")
+        if fmt == "mlx_q4":
+            qw, sc, bi = synth.numpy_mlx(N, K, gs, rng)
+            self.host = (qw, sc, bi)
+            self.w = torch.from_numpy(qw).to(dev)
+            self.scales, self.biases = torch.from_numpy(sc).to(dev), torch.from_numpy(bi).to(dev)
+            self.gs = gs
+            self.W = oq.dequant_mlx_q4(qw, sc, bi, gs)
+        else:
+            blob = synth.numpy_blocks(base, N, K, rng)
+            self.blob = blob
+            self.W = oq.dequant(base, blob, K)
+            if fmt == "q8_0_split":
+                qw, sc = oq.split_q8_0(blob, K)
+                self.w, self.scales = torch.from_numpy(qw).to(dev), torch.from_numpy(sc).to(dev)
+            elif fmt == "q5_0_split":
+                qw, qh, sc = oq.split_q5_0(blob, K)
+                self.w, self.aux, self.scales = (torch.from_numpy(a).to(dev) for a in (qw, qh, sc))
+            else:
+                self.w = torch.from_numpy(blob).to(dev)
+
+    def kw(self):
+        return dict(scales=self.scales, biases=self.biases, aux=self.aux, group_size=self.gs)
+
+    def qmm(self, x, **kw):
+        return alloy_amd.qmm(self.fmt, x, self.w, N=self.N, **self.kw(), **kw)
+
+    def dequant(self, **kw):
+        return alloy_amd.dequant(self.fmt, self.w, self.K, **self.kw(), **kw)
+
+
+def check(y, x, W, what):
+    ref = oq.ref_matmul(x, W)
+    rel, ratio = oq.parity_errors(y, ref, x, W)
+    assert rel <= REL_FRO and ratio <= MAX_RATIO, f"{what}: rel_fro={rel:.3e} max_ratio={ratio:.3e}"
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_dequant_bit_exact(dev, fmt):
+    rng = np.random.default_rng(11)
+    K = 1024 if fmt not in ("q4_k", "q6_k") else 1536
+    wt = Weight(fmt, 37, K, rng, dev)
+    got = wt.dequant().cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), wt.W.view(np.uint32)), f"{fmt} fp32 dequant not bit-exact"
+    got16 = wt.dequant(out_dtype=torch.float16).cpu().numpy()
+    assert np.array_equal(got16.view(np.uint16), wt.W.astype(np.float16).view(np.uint16)), f"{fmt} fp16 staging"
+    part = wt.dequant(rows=(5, 9)).cpu().numpy()
+    assert np.array_equal(part.view(np.uint32), wt.W[5:9].view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("N,K", [(203, 2048), (64, 3072), (130, 768)])
+def test_gemv_dot2_m1(dev, fmt, N, K):
+    if fmt in ("q4_k", "q6_k") and K % 256:
+        pytest.skip("K not a multiple of 256")
+    rng = np.random.default_rng(N + K)
+    wt = Weight(fmt, N, K, rng, dev)
+    x = synth.numpy_x(1, K, rng)
+    xt = torch.from_numpy(x).to(dev)
+    y = wt.qmm(xt, path="gemv", out_dtype=torch.float32).cpu().numpy()
+    check(y, x, wt.W, f"{fmt} gemv N={N} K={K}")
+    # every lanes-per-row variant gives the same answer
+    for L in (4, 8, 16, 32, 64):
+        yl = wt.qmm(xt, path="gemv", out_dtype=torch.float32, opts=L).cpu().numpy()
+        check(yl, x, wt.W, f"{fmt} gemv L={L}")
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_gemv_dot2_multi_row_and_f32_x(dev, fmt):
+    rng = np.random.default_rng(7)
+    N, K = 96, 1024
+    wt = Weight(fmt, N, K, rng, dev)
+    x = synth.numpy_x(3, K, rng)
+    y = wt.qmm(torch.from_numpy(x).to(dev), path="gemv", out_dtype=torch.float32).cpu().numpy()
+    check(y, x, wt.W, f"{fmt} gemv M=3")
+    x32 = rng.standard_normal((2, K)).astype(np.float32)
+    y32 = wt.qmm(torch.from_numpy(x32).to(dev), path="gemv").cpu().numpy()
+    check(y32, x32, wt.W, f"{fmt} gemv f32 activations")
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("M", [1, 4, 8, 16, 21])
+def test_gemv_mfma(dev, fmt, M):
+    rng = np.random.default_rng(M)
+    N, K = 150, 2560 if fmt not in ("q4_k", "q6_k") else 2304
+    wt = Weight(fmt, N, K, rng, dev)
+    x = synth.numpy_x(M, K, rng)
+    xt = torch.from_numpy(x).to(dev)
+    for rg in (1, 2):
+        y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=rg << 24).cpu().numpy()
+        check(y, x, wt.W, f"{fmt} gemv_mfma M={M} rg={rg}")
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("M,N,K", [(33, 130, 1024), (200, 256, 2048), (128, 64, 4096)])
+def test_gemm(dev, fmt, M, N, K):
+    rng = np.random.default_rng(M * N)
+    wt = Weight(fmt, N, K, rng, dev)
+    x = synth.numpy_x(M, K, rng)
+    y = wt.qmm(torch.from_numpy(x).to(dev), path="gemm", out_dtype=torch.float32).cpu().numpy()
+    check(y, x, wt.W, f"{fmt} gemm M={M} N={N} K={K}")
+
+
+def test_outputs_deterministic_and_f16(dev):
+    rng = np.random.default_rng(9)
+    wt = Weight("q4_k", 300, 4096, rng, dev)
+    for M, path in ((1, "gemv"), (8, "gemv_mfma"), (64, "gemm")):
+        x = torch.from_numpy(synth.numpy_x(M, 4096, rng)).to(dev)
+        a = wt.qmm(x, path=path, out_dtype=torch.float32)
+        b = wt.qmm(x, path=path, out_dtype=torch.float32)
+        assert torch.equal(a, b), f"{path} not deterministic"
+        h = wt.qmm(x, path=path)
+        assert h.dtype == torch.float16
+        assert torch.equal(h, a.to(torch.float16)), f"{path} fp16 output is not RN16 of the fp32 result"
+
+
+# ------------------------------------------------------------------ full benchmark shapes
+
+def _sampled(fmt, N, K, M, dev, seed, path="auto"):
+    """Run the kernel at the full shape; check sampled rows against the oracle."""
+    base = fmt.replace("_split", "")
+    w = synth.torch_blocks(base, N, K, seed, dev)
+    x = synth.torch_x(M, K, seed + 1, dev)
+    y = alloy_amd.qmm(base, x, w, out_dtype=torch.float32, path=path).cpu().numpy()
+    rng = np.random.default_rng(seed)
+    rows = np.unique(np.concatenate([rng.integers(0, N, 48), [0, N - 1]]))
+    blob = w[torch.from_numpy(rows).to(dev)].cpu().numpy()
+    W = oq.dequant(base, blob, K)
+    xs = x.cpu().numpy()
+    check(y[:, rows], xs, W, f"{fmt} {M}x{K}x{N} {path}")
+
+
+LLAMA32_3B = [(3072, 3072), (3072, 1024), (3072, 8192), (8192, 3072), (3072, 128256)]   # (K, N)
+LLAMA3_8B = [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)]
+
+
+@pytest.mark.parametrize("K,N", LLAMA32_3B)
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_q4_k_decode_shapes(dev, K, N, M):
+    _sampled("q4_k", N, K, M, dev, seed=K + N + M)
+
+
+@pytest.mark.parametrize("fmt", ["q6_k", "q5_0"])
+@pytest.mark.parametrize("K,N", LLAMA3_8B)
+@pytest.mark.parametrize("M", [1, 8])
+def test_q6_k_q5_0_decode_shapes(dev, fmt, K, N, M):
+    _sampled(fmt, N, K, M, dev, seed=K + 3 * N + M)
+
+
+def test_q8_0_config1(dev):
+    _sampled("q8_0", 4096, 4096, 1, dev, seed=0)
+
+
+@pytest.mark.parametrize("M", [512, 2048])
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 14336), (14336, 4096)])
+def test_q4_k_prefill_shapes(dev, M, K, N):
+    _sampled("q4_k", N, K, M, dev, seed=M + K + N, path="gemm")

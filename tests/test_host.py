@@ -1,0 +1,123 @@
+"""CPU tests of the host side: the C-ABI library loads and exports every declared
+symbol, its argument validation maps to the reference's exception types without
+touching a GPU, and the torch ops' Meta kernels / drop-in modules validate like
+the reference."""
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+import torch
+
+import alloy_amd
+from alloy_amd import _lib, formats
+from alloy_amd.modules import GGUFQ4_KLinear, GGUFQ8_0Linear, MLXQ4Linear
+
+HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "alloy_amd.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(alloy_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = alloy_amd.lib()
+    names = declared_functions()
+    assert "alloy_qmm" in names and len(names) >= 12
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signature table out of sync with the header"
+    assert lib.alloy_version().startswith(b"alloy_amd")
+
+
+def _qmm_status(fmt, K, M=1, N=4, w=16, x=16, y=16, gs=0, path=0, opts=0, xdt=1, scales=16, biases=16, aux=16):
+    lib = alloy_amd.lib()
+    vp = ctypes.c_void_p
+    return lib.alloy_qmm(_lib.FMT[fmt], vp(w), vp(aux), vp(scales), vp(biases), gs, vp(x), xdt, vp(y), 0,
+                         M, N, K, path, opts, None)
+
+
+def test_capi_validation_without_gpu():
+    # every case fails validation before any HIP call (fake, aligned pointers)
+    assert _qmm_status("q4_k", K=300) == _lib.E_SHAPE
+    assert _qmm_status("q4_k", K=256, w=8) == _lib.E_ALIGN
+    assert _qmm_status("q4_k", K=256, xdt=7) == _lib.E_DTYPE
+    assert _qmm_status("mlx_q4", K=256, gs=48) == _lib.E_SHAPE
+    assert _qmm_status("mlx_q4", K=256, gs=16) == _lib.E_UNSUPPORTED
+    assert _qmm_status("q4_k", K=256, path=9) == _lib.E_ARG
+    assert _qmm_status("q4_k", K=256, opts=3) == _lib.E_ARG
+    assert _qmm_status("q4_k", K=256, w=0) == _lib.E_ARG
+    assert _qmm_status("q4_k", K=256, M=0) == _lib.OK           # empty: nothing launched
+    with pytest.raises(ValueError, match="not divisible"):
+        _lib.check(_qmm_status("q6_k", K=100))
+    with pytest.raises(NotImplementedError):
+        _lib.check(_qmm_status("mlx_q4", K=256, gs=16))
+
+
+def test_moe_workspace_layout():
+    lib = alloy_amd.lib()
+    small = lib.alloy_moe_workspace_bytes(1, 128, 8, 2048, 768)
+    big = lib.alloy_moe_workspace_bytes(256, 128, 8, 2048, 768)
+    R = 256 * 8
+    assert big >= R * (2048 * 4 + 768 * 2) and big > small > 0
+    assert lib.alloy_moe_workspace_bytes(0, 0, 8, 2048, 768) == 0
+
+
+def meta(shape, dtype):
+    return torch.empty(shape, dtype=dtype, device="meta")
+
+
+def test_meta_shapes():
+    a = meta((5, 512), torch.float16)
+    assert torch.ops.alloy.gguf_q4_k_mm(a, meta((300, 288), torch.uint8)).shape == (5, 300)
+    assert torch.ops.alloy.gguf_q6_k_mm(a, meta((7, 420), torch.uint8)).shape == (5, 7)
+    assert torch.ops.alloy.gguf_q8_0_mm(a, meta((9, 512), torch.int8), meta((9, 16), torch.float16)).shape == (5, 9)
+    assert torch.ops.alloy.gguf_q5_0_mm(a, meta((9, 256), torch.uint8), meta((9, 256), torch.uint8),
+                                        meta((9, 16), torch.float16)).shape == (5, 9)
+    out = torch.ops.alloy.mlx_q4_mm(a, meta((11, 256), torch.uint8), meta((11, 8), torch.float16),
+                                    meta((11, 8), torch.float16))
+    assert out.shape == (5, 11) and out.dtype == torch.float16
+    assert torch.ops.alloy.gguf_q8_0_blocks_mm(a, meta((3, 16 * 34), torch.uint8)).shape == (5, 3)
+    outs = torch.ops.alloy.batched_gguf_q4_k_mm(a, [meta((4, 288), torch.uint8), meta((6, 288), torch.uint8)])
+    assert [o.shape for o in outs] == [(5, 4), (5, 6)]
+    E, H, I = 4, 256, 64
+    y = torch.ops.alloy.mlx_moe_routed(meta((3, H), torch.float16), meta((3, E), torch.float32),
+                                       meta((E, 2 * I, H // 2), torch.uint8), meta((E, 2 * I, H // 64), torch.float16),
+                                       meta((E, 2 * I, H // 64), torch.float16), meta((E, H, I // 2), torch.uint8),
+                                       meta((E, H, I // 64), torch.float16), meta((E, H, I // 64), torch.float16),
+                                       E, 2, I)
+    assert y.shape == (3, H) and y.dtype == torch.float32
+
+
+def test_meta_validation_errors():
+    a = meta((5, 512), torch.float16)
+    with pytest.raises(ValueError):
+        torch.ops.alloy.gguf_q4_k_mm(a, meta((3, 144), torch.uint8))         # wrong row bytes
+    with pytest.raises(TypeError):
+        torch.ops.alloy.gguf_q4_k_mm(a, meta((3, 288), torch.int8))          # wrong dtype
+    with pytest.raises(TypeError):
+        torch.ops.alloy.gguf_q4_k_mm(meta((5, 512), torch.bfloat16), meta((3, 288), torch.uint8))
+
+
+def test_ops_refuse_cpu_tensors():
+    a = torch.zeros((1, 256), dtype=torch.float16)
+    with pytest.raises((RuntimeError, NotImplementedError)):
+        torch.ops.alloy.gguf_q4_k_mm(a, torch.zeros((2, 144), dtype=torch.uint8))
+
+
+def test_module_validation_matches_reference():
+    with pytest.raises(ValueError, match="not divisible"):
+        GGUFQ4_KLinear(in_features=100, out_features=2, blocks=torch.zeros((2, 144), dtype=torch.uint8))
+    with pytest.raises(TypeError):
+        GGUFQ8_0Linear(in_features=64, out_features=2, qweight=torch.zeros((2, 64), dtype=torch.uint8),
+                       scales=torch.zeros((2, 2), dtype=torch.float16))
+    with pytest.raises(ValueError, match="expects buffers"):
+        GGUFQ8_0Linear(in_features=64, out_features=2, qweight=torch.zeros((2, 64), dtype=torch.int8))
+    with pytest.raises(ValueError, match="group size"):
+        MLXQ4Linear(in_features=64, out_features=2, qweight=torch.zeros((2, 32), dtype=torch.uint8),
+                    scales=torch.zeros((2, 3), dtype=torch.float16), biases=torch.zeros((2, 3), dtype=torch.float16))
+    m = GGUFQ4_KLinear(in_features=512, out_features=3, blocks=torch.zeros((3, 288), dtype=torch.uint8))
+    assert m.blocks.shape == (3, 288)
+    assert formats.row_bytes("q6_k", 4096) == 3360
