@@ -114,18 +114,19 @@ alloy_status alloy_qmm(alloy_format fmt, const void* w, const void* aux, const v
   if (!aligned(x, 16)) return fail(ALLOY_E_ALIGN, "activations not 16-byte aligned");
   if (!aligned(y, y_dtype == ALLOY_DT_F32 ? 4 : 2)) return fail(ALLOY_E_ALIGN, "output misaligned");
   alloy::Opts o;
-  o.lanes_per_row = (int)(opts & 0xFF);
-  o.grid_cap = (int)((opts >> 8) & 0xFFFF);
-  o.row_groups = (int)((opts >> 24) & 0xF);
-  if (o.lanes_per_row && (o.lanes_per_row & (o.lanes_per_row - 1) || o.lanes_per_row < 4 || o.lanes_per_row > 64))
-    return fail(ALLOY_E_ARG, "lanes_per_row %d must be a power of two in [4, 64]", o.lanes_per_row);
+  o.lanes_per_row = (int)(opts & 0xFFF);
+  o.grid_cap = (int)((opts >> 12) & 0xFFFF);
+  o.row_groups = (int)((opts >> 28) & 0xF);
+  o.depth = (int)((opts >> 32) & 0xF);
+  if (o.lanes_per_row && (o.lanes_per_row % 16 || o.lanes_per_row > 256))
+    return fail(ALLOY_E_ARG, "lanes_per_row %d must be a multiple of 16 in [16, 256]", o.lanes_per_row);
   int p = (int)path;
-  if (p == ALLOY_PATH_AUTO) p = (M == 1 && K <= alloy::kMaxKDot2) ? alloy::P_GEMV : (M <= 16 ? alloy::P_GEMV_MFMA : alloy::P_GEMM);
+  if (p == ALLOY_PATH_AUTO) p = (M == 1 && K <= alloy::max_k_dot2((int)fmt)) ? alloy::P_GEMV : (M <= 16 ? alloy::P_GEMV_MFMA : alloy::P_GEMM);
   const bool xf = x_dtype == ALLOY_DT_F32, yf = y_dtype == ALLOY_DT_F32;
   hipStream_t st = (hipStream_t)stream;
   switch (p) {
     case alloy::P_GEMV:
-      if (K > alloy::kMaxKDot2) return fail(ALLOY_E_UNSUPPORTED, "v_dot2 GEMV: K=%lld exceeds %lld", (long long)K, (long long)alloy::kMaxKDot2);
+      if (K > alloy::max_k_dot2((int)fmt)) return fail(ALLOY_E_UNSUPPORTED, "v_dot2 GEMV: K=%lld exceeds %lld", (long long)K, (long long)alloy::max_k_dot2((int)fmt));
       if (M > 65535) return fail(ALLOY_E_SHAPE, "v_dot2 GEMV: M=%lld too large", (long long)M);
       return hip_status(alloy::launch_gemv_dot2((int)fmt, a, x, xf, y, yf, M, N, o, st), "gemv_dot2 launch");
     case alloy::P_GEMV_MFMA:

@@ -68,29 +68,43 @@ __global__ __launch_bounds__(256) void k_dequant(QArgs a, void* out, int out_f16
 }
 
 // ------------------------------------------------------------------ M=1 GEMV (v_dot2)
-// x is staged once per workgroup into LDS as fp16 pairs in the format's XPERM order,
-// plus fp32 sums per 16 elements.  L lanes cooperate on one row (units strided by L),
-// so a wave covers 64/L rows per step; rows are grid-strided.  grid.y = x row.
-template <int XPERM, typename XT>
-__device__ __forceinline__ void stage_x(const XT* x, int K, uint32_t* xs, float* xs16) {
-  for (int g = threadIdx.x; g < (K >> 4); g += blockDim.x) {
-    f16x8 lo = ld_x8<XT>(x + 16 * g), hi = ld_x8<XT>(x + 16 * g + 8);
-    f16 v[16];
+// Each thread owns UPT decode units of the row (the same units for every row it
+// visits) and keeps their x values in registers: fp16 pairs in the format's XPERM
+// order plus fp32 sums per 16 elements.  L threads cover one row (L >= units per
+// row / UPT), so a 256-thread workgroup works on 256/L rows at a time and walks
+// its rows with a grid stride; the next row's weight bytes are loaded while the
+// current row is computed.  Row sums are reduced in a fixed order (shuffles inside
+// a wave, then LDS across waves).  grid.y = activation row.
+template <class F, typename XT>
+__device__ __forceinline__ void load_x_unit(const XT* x, int u, uint32_t (&xr)[F::UE / 2],
+                                            float (&xg)[F::UE / 16]) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) { v[e] = lo[e]; v[8 + e] = hi[e]; }
-    float s = 0.f;
+  for (int r = 0; r < F::UE / 32; ++r) {
+    const XT* p = x + F::run_start(u, r);
+    f16 v[32];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) s += (float)v[e];
-    uint32_t o[8];
-    if (XPERM == 4) {
+    for (int c = 0; c < 4; ++c) {
+      const f16x8 t = ld_x8<XT>(p + 8 * c);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int e = 0; e < 8; ++e) v[8 * c + e] = t[e];
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sum += (float)v[16 * h + e];
+      xg[2 * r + h] = sum;
+    }
+    uint32_t* o = xr + 16 * r;
+    if (F::XPERM == 4) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
         o[2 * j] = pack2(v[4 * j], v[4 * j + 2]);
         o[2 * j + 1] = pack2(v[4 * j + 1], v[4 * j + 3]);
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < 4; ++j) {
         const int b = 8 * j;
         o[4 * j] = pack2(v[b], v[b + 4]);
         o[4 * j + 1] = pack2(v[b + 2], v[b + 6]);
@@ -98,38 +112,89 @@ __device__ __forceinline__ void stage_x(const XT* x, int K, uint32_t* xs, float*
         o[4 * j + 3] = pack2(v[b + 3], v[b + 7]);
       }
     }
-    *(u32x4*)(xs + 8 * g) = u32x4{o[0], o[1], o[2], o[3]};
-    *(u32x4*)(xs + 8 * g + 4) = u32x4{o[4], o[5], o[6], o[7]};
-    xs16[g] = s;
   }
 }
 
-template <class F, int L, typename XT>
+// L = 16*C16 threads cover one row (each owns UPT units); a workgroup of
+// R*L threads (R = 16/C16) works on R rows per step.  D rows of weights are in
+// flight per thread in a ring of D register slots, unrolled so every slot is a fixed
+// set of registers: slot d is computed, then immediately refilled with the row D
+// steps ahead.  Refills are unconditional (row and unit indices clamped into range)
+// so the compiler never has to merge old and new slot contents, which would force
+// a wait on the load just issued.  Row sums: 16-lane shuffles, then the C16 partial
+// sums of a row are added in order through LDS.
+template <class F, int UPT, int D, typename XT>
 __global__ __launch_bounds__(256) void k_gemv_dot2(QArgs a, const XT* x, void* y, int y_f32,
-                                                   int64_t N) {
-  extern __shared__ uint32_t smem[];
-  const int K = a.K;
-  uint32_t* xs = smem;
-  float* xs16 = (float*)(smem + (K >> 1));
+                                                   int64_t N, int C16) {
+  __shared__ float red[2][16];
+  const int L = 16 * C16;
+  const int R = blockDim.x / L;
+  const int K = a.K, U = K / F::UE;
+  const int t = threadIdx.x, slot = t / L, li = t - slot * L;
   const int64_t m = blockIdx.y;
-  stage_x<F::XPERM, XT>(x + m * K, K, xs, xs16);
-  __syncthreads();
+  bool own[UPT];
+  int uu[UPT];
+#pragma unroll
+  for (int j = 0; j < UPT; ++j) {
+    own[j] = li + L * j < U;
+    uu[j] = own[j] ? li + L * j : U - 1;     // clamped unit: always a valid address
+  }
+  const int64_t stride = (int64_t)gridDim.x * R;
+  const int64_t nb0 = (int64_t)blockIdx.x * R;
+  auto clamp_row = [&](int64_t n) { return n < N ? n : N - 1; };
+  typename F::Raw ring[D][UPT];
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+#pragma unroll
+    for (int j = 0; j < UPT; ++j) ring[d][j] = F::load(a, clamp_row(nb0 + d * stride + slot), uu[j]);
+  uint32_t xr[UPT][F::UE / 2];
+  float xg[UPT][F::UE / 16];
+  const XT* xm = x + m * K;
+#pragma unroll
+  for (int j = 0; j < UPT; ++j) load_x_unit<F, XT>(xm, uu[j], xr[j], xg[j]);
 
-  constexpr int RPW = 64 / L;
-  const int U = K / F::UE;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int sub = lane / L, li = lane % L;
-  const int64_t step = (int64_t)gridDim.x * 4 * RPW;
-  for (int64_t n0 = ((int64_t)blockIdx.x * 4 + wave) * RPW; n0 < N; n0 += step) {
-    const int64_t n = n0 + sub;
+  int par = 0;
+  // Sum of slot d's row (all lanes of the row end with the sum), then refill slot d.
+  auto step = [&](int d, int64_t n) {
     float acc = 0.f;
-    if (n < N) {
-#pragma unroll 4
-      for (int u = li; u < U; u += L) acc += F::unit_dot(a, n, u, xs, xs16);
+#pragma unroll
+    for (int j = 0; j < UPT; ++j) {
+      const float v = F::dot(ring[d][j], uu[j], xr[j], xg[j]);
+      acc += own[j] ? v : 0.f;
     }
 #pragma unroll
-    for (int off = L / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    if (li == 0 && n < N) store_y(y, y_f32, m * N + n, acc);
+    for (int j = 0; j < UPT; ++j) ring[d][j] = F::load(a, clamp_row(n + D * stride), uu[j]);
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (C16 > 1) {
+      if ((li & 15) == 0) red[par][slot * C16 + (li >> 4)] = acc;
+      __syncthreads();
+      acc = 0.f;
+      for (int g = 0; g < C16; ++g) acc += red[par][slot * C16 + g];
+      par ^= 1;
+    }
+    return acc;
+  };
+  int64_t base = nb0;
+  // full blocks: every row of every slot is in range, every lane stores its row sum
+  for (; base + (int64_t)(D - 1) * stride + R <= N; base += D * stride) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int64_t n = base + d * stride + slot;
+      const float v = step(d, n);
+      store_y(y, y_f32, m * N + n, v);
+    }
+  }
+  // tail
+  for (; base < N; base += D * stride) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int64_t nbd = base + d * stride;     // uniform
+      if (nbd >= N) break;
+      const int64_t n = nbd + slot;
+      const float v = step(d, n);
+      if (li == 0 && n < N) store_y(y, y_f32, m * N + n, v);
+    }
   }
 }
 
@@ -320,46 +385,36 @@ static int pow2_floor(int v) {
 
 template <class F>
 struct GemvDot2Run {
-  template <int L, typename XT>
+  template <int UPT, typename XT>
   static hipError_t go(const QArgs& a, const void* x, void* y, bool y_f32, int64_t M, int64_t N,
-                       int grid_cap, hipStream_t st) {
-    const size_t shm = (size_t)a.K * 2 + (size_t)(a.K / 16) * 4;
-    auto kfn = k_gemv_dot2<F, L, XT>;
-    if (shm > 65536) {
-      hipError_t e = hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-      if (e != hipSuccess) return e;
-    }
-    const int64_t rows_per_iter = 4 * (64 / L);
-    int64_t grid = (N + rows_per_iter - 1) / rows_per_iter;
-    const int64_t cap = grid_cap > 0 ? grid_cap : 2048;
+                       int C16, int grid_cap, int depth, hipStream_t st) {
+    const int R = 16 / C16;
+    int64_t grid = (N + R - 1) / R;
+    const int64_t cap = grid_cap > 0 ? grid_cap : 1024;
     if (grid > cap) grid = cap;
-    if (grid < 1) grid = 1;
-    hipLaunchKernelGGL(kfn, dim3((unsigned)grid, (unsigned)M), dim3(256), shm, st, a,
-                       (const XT*)x, y, (int)y_f32, N);
+    const dim3 g((unsigned)grid, (unsigned)M), b(16 * C16 * R);
+    if (depth == 2)
+      hipLaunchKernelGGL((k_gemv_dot2<F, UPT, 2, XT>), g, b, 0, st, a, (const XT*)x, y, (int)y_f32, N, C16);
+    else if (depth == 4)
+      hipLaunchKernelGGL((k_gemv_dot2<F, UPT, 4, XT>), g, b, 0, st, a, (const XT*)x, y, (int)y_f32, N, C16);
+    else
+      hipLaunchKernelGGL((k_gemv_dot2<F, UPT, 3, XT>), g, b, 0, st, a, (const XT*)x, y, (int)y_f32, N, C16);
     return hipGetLastError();
-  }
-  template <typename XT>
-  static hipError_t pick(int L, const QArgs& a, const void* x, void* y, bool y_f32, int64_t M,
-                         int64_t N, int cap, hipStream_t st) {
-    switch (L) {
-      case 4: return go<4, XT>(a, x, y, y_f32, M, N, cap, st);
-      case 8: return go<8, XT>(a, x, y, y_f32, M, N, cap, st);
-      case 16: return go<16, XT>(a, x, y, y_f32, M, N, cap, st);
-      case 32: return go<32, XT>(a, x, y, y_f32, M, N, cap, st);
-      default: return go<64, XT>(a, x, y, y_f32, M, N, cap, st);
-    }
   }
   static hipError_t run(const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32, int64_t M,
                         int64_t N, const Opts& o, hipStream_t st) {
     const int U = a.K / F::UE;
-    int L = o.lanes_per_row;
-    if (L <= 0) {
-      L = pow2_floor(U / 3 > 0 ? U / 3 : 1);
-      if (L < 4) L = 4;
-      if (L > 64) L = 64;
+    // threads per row: one unit each when U <= 256, else two; in groups of 16
+    int upt = U > 256 ? 2 : 1;
+    int C16 = ((U + upt - 1) / upt + 15) / 16;
+    if (o.lanes_per_row >= 16) {                     // explicit override (tuning / tests)
+      const int c = o.lanes_per_row / 16;
+      if (c * 16 * 2 >= U) { C16 = c > 16 ? 16 : c; upt = C16 * 16 >= U ? 1 : 2; }
     }
-    return x_f32 ? pick<float>(L, a, x, y, y_f32, M, N, o.grid_cap, st)
-                 : pick<f16>(L, a, x, y, y_f32, M, N, o.grid_cap, st);
+    if (upt == 2) return x_f32 ? go<2, float>(a, x, y, y_f32, M, N, C16, o.grid_cap, o.depth, st)
+                               : go<2, f16>(a, x, y, y_f32, M, N, C16, o.grid_cap, o.depth, st);
+    return x_f32 ? go<1, float>(a, x, y, y_f32, M, N, C16, o.grid_cap, o.depth, st)
+                 : go<1, f16>(a, x, y, y_f32, M, N, C16, o.grid_cap, o.depth, st);
   }
 };
 

@@ -13,9 +13,10 @@ enum Path : int { P_AUTO = 0, P_GEMV = 1, P_GEMV_MFMA = 2, P_GEMM = 3 };
 
 // Launch-shape knobs (0 = automatic choice).
 struct Opts {
-  int lanes_per_row = 0;   // dot2 GEMV: lanes cooperating on one row (4..64)
+  int lanes_per_row = 0;   // dot2 GEMV: threads cooperating on one row (multiple of 16, <= 256)
   int grid_cap = 0;        // dot2 GEMV: max workgroups (grid-stride beyond)
   int row_groups = 0;      // MFMA GEMV: 16-row groups per workgroup (1, 2)
+  int depth = 0;           // dot2 GEMV: rows of weights in flight per thread (2, 3, 4)
 };
 
 hipError_t launch_dequant(int fmt, const QArgs& a, void* out, bool out_f16, int64_t row0,
@@ -27,7 +28,8 @@ hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, 
 hipError_t launch_gemm(int fmt, const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32,
                        int64_t M, int64_t N, const Opts& o, hipStream_t st);
 
-// dot2 GEMV stages x (K fp16 + K/16 fp32 sums) in LDS.
-constexpr int64_t kMaxKDot2 = 32768;
+// The v_dot2 GEMV gives each thread at most 2 decode units of a 256-thread row:
+// K <= 512 units per row.
+inline int64_t max_k_dot2(int fmt) { return (fmt == F_Q4_K || fmt == F_Q6_K) ? 512 * 64 : 512 * 32; }
 
 }  // namespace alloy

@@ -6,14 +6,16 @@
 //                            so Q8_0/Q5_0/Q6_K are exact and Q4_K/MLX are rounded
 //                            once — the values are bit-identical to the reference's
 //                            fp32 decode whatever the operation order.
-//   unit_dot(a, n, u, xs, xs16)
-//                            sum_e w_e * x_e over decode unit u of row n, for the
-//                            M=1 GEMV.  Quants are turned into fp16 "1 + q/2^b"
-//                            values by placing the b-bit quant in the top mantissa
-//                            bits of 0x3C00 (exact), dotted with x by v_dot2_f32_f16
-//                            (products exact, fp32 accumulation), and the 1.0 bias
-//                            is removed with the per-16-element x sums xs16.
-//                            xs holds x as fp16 pairs in the format's XPERM order.
+//   load(a, n, u) -> Raw     the raw bytes of decode unit u of row n (registers)
+//   dot(raw, xr, xs16)       sum_e w_e * x_e over that unit, for the M=1 GEMV.
+//                            Quants are turned into fp16 "1 + q/2^b" values by
+//                            placing the b-bit quant in the top mantissa bits of
+//                            0x3C00 (exact), dotted with x by v_dot2_f32_f16
+//                            (products exact, fp32 accumulation); the 1.0 bias is
+//                            removed with the per-16-element x sums xs16.  xr holds
+//                            the unit's x as fp16 pairs in the format's XPERM order,
+//                            one 32-element run after the other (run_start gives
+//                            the first element of each run).
 //   constants QK (block elements), UE (unit elements), XPERM (4 or 8).
 //
 // Layout citations (reference, read-only):
@@ -59,9 +61,10 @@ __device__ __forceinline__ uint32_t ldu16(const void* p) { return *(const uint16
 // in [p - 2, p + 4*NW): aligned dword loads plus one u16 load, then v_alignbyte.
 template <int NW>
 __device__ __forceinline__ void ld_words_a2(const uint8_t* p, uint32_t (&o)[NW]) {
-  const uintptr_t a = (uintptr_t)p;
-  const uint32_t* q = (const uint32_t*)(a & ~(uintptr_t)3);
-  const uint32_t sh = (uint32_t)(a & 2);      // byte shift: 0 or 2
+  const uint32_t sh = (uint32_t)((uintptr_t)p & 2);   // byte shift: 0 or 2
+  // pointer arithmetic (not an integer round trip) keeps the global address space,
+  // so these stay global_load instructions rather than FLAT ones
+  const uint32_t* q = (const uint32_t*)(p - sh);
   uint32_t t[NW + 1];
 #pragma unroll
   for (int i = 0; i < NW; ++i) t[i] = q[i];
@@ -72,6 +75,34 @@ __device__ __forceinline__ void ld_words_a2(const uint8_t* p, uint32_t (&o)[NW])
 
 // fp16 pair constants
 #define MAGIC1 0x3C003C00u   // fp16 1.0 in both halves
+
+// Bit-field helpers emitted as single VOP3 instructions (the mask lives in an SGPR,
+// the other operands in VGPRs: one constant-bus read, as gfx9 allows).
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {   // (a & mask) | (b & ~mask)
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t b) { // (a & mask) | b
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(b));
+  return r;
+}
+template <int SH>
+__device__ __forceinline__ uint32_t lshl_or(uint32_t a, uint32_t b) {                // (a << SH) | b
+  uint32_t r;
+  asm("v_lshl_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "i"(SH), "v"(b));
+  return r;
+}
+
+// The four fp16 pairs "1 + q/16" of the 8 nibbles of v, in the order
+// (byte0 lo, byte2 lo), (byte1 lo, byte3 lo), (byte0 hi, byte2 hi), (byte1 hi, byte3 hi).
+__device__ __forceinline__ void nib_pairs(uint32_t v, uint32_t magic, uint32_t (&p)[4]) {
+  p[0] = lshl_or<6>(v & 0x000F000Fu, magic);
+  p[1] = bfi(0x03C003C0u, v >> 2, magic);
+  p[2] = lshl_or<2>(v & 0x00F000F0u, magic);
+  p[3] = bfi(0x03C003C0u, v >> 6, magic);
+}
 
 // ------------------------------------------------------------------ Q4_K
 // 144 B: fp16 d | fp16 dmin | scales[12] | qs[128]; sub-block g (32 el) uses
@@ -88,6 +119,30 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t S0, uint32_t S1, uint32_t
     m = ((S2 >> (j + 4)) & 0xFu) | (((S1 >> (j + 6)) & 3u) << 4);
   }
 }
+
+// Branch-free get_scale_min_k4 for a sub-block index that differs across lanes:
+// the bit offsets/widths are precomputed once per lane (Q4kSel), then each block
+// costs two selects, four bit-field extracts and two shifts-with-or.
+struct Q4kSel {
+  uint32_t hi;            // 1 when g >= 4
+  uint32_t sc_sh, m_sh;   // offset of the low bits of sc / m
+  uint32_t lo_w;          // 6 (g < 4) or 4 (g >= 4)
+  uint32_t top_sh, top_w; // offset / width (0 or 2) of the top 2 bits in S0 / S1
+  __device__ explicit Q4kSel(int g) {
+    hi = g >= 4;
+    const int j = 8 * (g & 3);
+    sc_sh = hi ? j : 8 * g;
+    m_sh = hi ? j + 4 : 8 * g;
+    lo_w = hi ? 4 : 6;
+    top_sh = j + 6;
+    top_w = hi ? 2 : 0;
+  }
+  __device__ __forceinline__ void get(uint32_t S0, uint32_t S1, uint32_t S2, uint32_t& sc, uint32_t& m) const {
+    const uint32_t lsc = hi ? S2 : S0, lm = hi ? S2 : S1;
+    sc = lshl_or<4>(__builtin_amdgcn_ubfe(S0, top_sh, top_w), __builtin_amdgcn_ubfe(lsc, sc_sh, lo_w));
+    m = lshl_or<4>(__builtin_amdgcn_ubfe(S1, top_sh, top_w), __builtin_amdgcn_ubfe(lm, m_sh, lo_w));
+  }
+};
 
 struct FQ4K {
   static constexpr int QK = 256, BB = 144, UE = 64, XPERM = 4;
@@ -112,31 +167,35 @@ struct FQ4K {
   }
 
   // unit u = (superblock u/4, pair p = u%4): sub-blocks 2p (low nibbles) and 2p+1.
-  __device__ static float unit_dot(const QArgs& a, int64_t n, int u, const uint32_t* xs,
-                                   const float* xs16) {
-    const int p = u & 3;
+  // unit u = (superblock u/4, pair p = u%4): sub-blocks 2p (low nibbles) and 2p+1;
+  // runs: elements 64u + [0,32) and 64u + 32 + [0,32).
+  struct Raw { u32x4 h, q0, q1; };
+  __device__ static int run_start(int u, int r) { return 64 * u + 32 * r; }
+  __device__ static Raw load(const QArgs& a, int64_t n, int u) {
     const uint8_t* blk = a.w + n * a.rb + (int64_t)(u >> 2) * BB;
-    const u32x4 h = ld16(blk);
-    const u32x4 q0 = ld16(blk + 16 + 32 * p), q1 = ld16(blk + 32 + 32 * p);
-    const uint32_t words[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    const int e0 = 64 * u;                       // first element of the unit in the row
-    const uint32_t* xa = xs + (e0 >> 1);        // sub-block A pairs (perm4)
+    const int p = u & 3;
+    return Raw{ld16(blk), ld16(blk + 16 + 32 * p), ld16(blk + 32 + 32 * p)};
+  }
+  __device__ static float dot(const Raw& r, int u, const uint32_t* xa, const float* xg) {
+    const int p = u & 3;
+    const uint32_t words[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
     const uint32_t* xb = xa + 16;                // sub-block B pairs
+    const uint32_t magic = MAGIC1;
     float SA = 0.f, SB = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const uint32_t v = words[i];
-      SA = dot2(((v << 6) & 0x03C003C0u) | MAGIC1, xa[2 * i], SA);
-      SA = dot2(((v >> 2) & 0x03C003C0u) | MAGIC1, xa[2 * i + 1], SA);
-      SB = dot2(((v << 2) & 0x03C003C0u) | MAGIC1, xb[2 * i], SB);
-      SB = dot2(((v >> 6) & 0x03C003C0u) | MAGIC1, xb[2 * i + 1], SB);
+      uint32_t pr[4];
+      nib_pairs(words[i], magic, pr);
+      SA = dot2(pr[0], xa[2 * i], SA);
+      SA = dot2(pr[1], xa[2 * i + 1], SA);
+      SB = dot2(pr[2], xb[2 * i], SB);
+      SB = dot2(pr[3], xb[2 * i + 1], SB);
     }
-    const float* xg = xs16 + (e0 >> 4);
     const float XA = xg[0] + xg[1], XB = xg[2] + xg[3];
-    const float d16 = 16.f * h2f(h.x), dmin = h2f(h.x >> 16);
+    const float d16 = 16.f * h2f(r.h.x), dmin = h2f(r.h.x >> 16);
     uint32_t scA, mA, scB, mB;
-    q4k_scale_min(h.y, h.z, h.w, 2 * p, scA, mA);
-    q4k_scale_min(h.y, h.z, h.w, 2 * p + 1, scB, mB);
+    Q4kSel(2 * p).get(r.h.y, r.h.z, r.h.w, scA, mA);
+    Q4kSel(2 * p + 1).get(r.h.y, r.h.z, r.h.w, scB, mB);
     const float cA = d16 * (float)scA, cB = d16 * (float)scB;
     // sum(q x) = 16 (S - X);  w = d sc q - dmin m
     return cA * SA - (cA + dmin * (float)mA) * XA + cB * SB - (cB + dmin * (float)mB) * XB;
@@ -171,54 +230,60 @@ struct FQ6K {
 
   // unit u = (superblock u/4, half h = (u%4)/2, s0 = u%2): elements
   // 128h+32*s0+l (low nibbles) and 128h+32*(s0+2)+l (high nibbles), l in [0,32).
-  __device__ static float unit_dot(const QArgs& a, int64_t n, int u, const uint32_t* xs,
-                                   const float* xs16) {
+  // unit u = (superblock u/4, half h = (u%4)/2, s0 = u%2): runs of elements
+  // 128h+32*s0+l (low nibbles) and 128h+32*(s0+2)+l (high nibbles), l in [0,32).
+  struct Raw { uint32_t ql[8], qh[8], scl, sch, d; };
+  __device__ static int run_start(int u, int r) {
+    return 256 * (u >> 2) + 128 * ((u >> 1) & 1) + 32 * (u & 1) + 64 * r;
+  }
+  __device__ static Raw load(const QArgs& a, int64_t n, int u) {
     const int h = (u >> 1) & 1, s0 = u & 1;
     const uint8_t* blk = a.w + n * a.rb + (int64_t)(u >> 2) * BB;
-    uint32_t ql[8], qh[8];
-    ld_words_a2<8>(blk + 64 * h + 32 * s0, ql);
-    ld_words_a2<8>(blk + 128 + 32 * h, qh);
-    const uint32_t scl = ldu16(blk + 192 + 8 * h + 2 * s0);       // scales (s0, l<16), (s0, l>=16)
-    const uint32_t sch = ldu16(blk + 192 + 8 * h + 2 * s0 + 4);   // scales (s0+2, ...)
-    const float d = h2f(ldu16(blk + 208));
-    const int eb = 256 * (u >> 2) + 128 * h;
-    const uint32_t* xlo = xs + ((eb + 32 * s0) >> 1);
-    const uint32_t* xhi = xs + ((eb + 32 * s0 + 64) >> 1);
-    const int c0 = 2 * s0;
+    Raw r;
+    ld_words_a2<8>(blk + 64 * h + 32 * s0, r.ql);
+    ld_words_a2<8>(blk + 128 + 32 * h, r.qh);
+    r.scl = ldu16(blk + 192 + 8 * h + 2 * s0);       // scales (s0, l<16), (s0, l>=16)
+    r.sch = ldu16(blk + 192 + 8 * h + 2 * s0 + 4);   // scales (s0+2, ...)
+    r.d = ldu16(blk + 208);
+    return r;
+  }
+  __device__ static float dot(const Raw& r, int u, const uint32_t* xlo, const float* xg) {
+    const int c0 = 2 * (u & 1);
+    const uint32_t magic = MAGIC1;
+    const uint32_t* xhi = xlo + 16;
     float S[4] = {0.f, 0.f, 0.f, 0.f};   // (s0,l<16) (s0,l>=16) (s0+2,l<16) (s0+2,l>=16)
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const uint32_t v = ql[i], c = qh[i];
+      const uint32_t v = r.ql[i], c = r.qh[i];
       // 6-bit u in fp16 mantissa bits 4..9 -> value 1 + u/64
-      const uint32_t p0 = ((v << 4) & 0x00F000F0u) | ((c << (8 - c0)) & 0x03000300u) | MAGIC1;
-      const uint32_t p1 = ((v >> 4) & 0x00F000F0u) | ((c >> c0) & 0x03000300u) | MAGIC1;
-      const uint32_t p2 = (v & 0x00F000F0u) | ((c << (4 - c0)) & 0x03000300u) | MAGIC1;
-      const uint32_t p3 = ((v >> 8) & 0x00F000F0u) | ((c >> (c0 + 4)) & 0x03000300u) | MAGIC1;
-      const int r = i >> 2;
-      S[r] = dot2(p0, xlo[2 * i], S[r]);
-      S[r] = dot2(p1, xlo[2 * i + 1], S[r]);
-      S[2 + r] = dot2(p2, xhi[2 * i], S[2 + r]);
-      S[2 + r] = dot2(p3, xhi[2 * i + 1], S[2 + r]);
+      const uint32_t p0 = bfi(0x03000300u, c << (8 - c0), bfi(0x00F000F0u, v << 4, magic));
+      const uint32_t p1 = bfi(0x03000300u, c >> c0, bfi(0x00F000F0u, v >> 4, magic));
+      const uint32_t p2 = bfi(0x03000300u, c << (4 - c0), and_or(v, 0x00F000F0u, magic));
+      const uint32_t p3 = bfi(0x03000300u, c >> (c0 + 4), bfi(0x00F000F0u, v >> 8, magic));
+      const int q = i >> 2;
+      S[q] = dot2(p0, xlo[2 * i], S[q]);
+      S[q] = dot2(p1, xlo[2 * i + 1], S[q]);
+      S[2 + q] = dot2(p2, xhi[2 * i], S[2 + q]);
+      S[2 + q] = dot2(p3, xhi[2 * i + 1], S[2 + q]);
     }
-    const float* xl = xs16 + ((eb + 32 * s0) >> 4);
-    const float* xh = xs16 + ((eb + 32 * s0 + 64) >> 4);
     // sum((u-32) x) = 64 S - 96 X
-    float acc = (float)(int8_t)(scl & 0xFF) * (64.f * S[0] - 96.f * xl[0]);
-    acc += (float)(int8_t)(scl >> 8) * (64.f * S[1] - 96.f * xl[1]);
-    acc += (float)(int8_t)(sch & 0xFF) * (64.f * S[2] - 96.f * xh[0]);
-    acc += (float)(int8_t)(sch >> 8) * (64.f * S[3] - 96.f * xh[1]);
-    return d * acc;
+    float acc = (float)(int8_t)(r.scl & 0xFF) * (64.f * S[0] - 96.f * xg[0]);
+    acc += (float)(int8_t)(r.scl >> 8) * (64.f * S[1] - 96.f * xg[1]);
+    acc += (float)(int8_t)(r.sch & 0xFF) * (64.f * S[2] - 96.f * xg[2]);
+    acc += (float)(int8_t)(r.sch >> 8) * (64.f * S[3] - 96.f * xg[3]);
+    return h2f(r.d) * acc;
   }
 };
 
 // ------------------------------------------------------------------ Q8_0 (wire)
 // 34 B: fp16 d | int8 qs[32]; w = d*q.
 __device__ __forceinline__ float q8_words_dot(const uint32_t (&v)[8], const uint32_t* xp, float S) {
+  const uint32_t magic = MAGIC1;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const uint32_t o = v[i] ^ 0x80808080u;       // offset binary u = q + 128
-    S = dot2(((o << 2) & 0x03FC03FCu) | MAGIC1, xp[2 * i], S);       // bytes 0,2 -> 1 + u/256
-    S = dot2(((o >> 6) & 0x03FC03FCu) | MAGIC1, xp[2 * i + 1], S);   // bytes 1,3
+    S = dot2(lshl_or<2>(o & 0x00FF00FFu, magic), xp[2 * i], S);      // bytes 0,2 -> 1 + u/256
+    S = dot2(bfi(0x03FC03FCu, o >> 6, magic), xp[2 * i + 1], S);     // bytes 1,3
   }
   return S;
 }
@@ -237,15 +302,18 @@ struct FQ80 {
       for (int b = 0; b < 4; ++b) w[4 * i + b] = d * (float)(int8_t)((v[i] >> (8 * b)) & 0xFF);
   }
 
-  __device__ static float unit_dot(const QArgs& a, int64_t n, int u, const uint32_t* xs,
-                                   const float* xs16) {
+  struct Raw { uint32_t v[8]; uint32_t d; };
+  __device__ static int run_start(int u, int) { return 32 * u; }
+  __device__ static Raw load(const QArgs& a, int64_t n, int u) {
     const uint8_t* blk = a.w + n * a.rb + (int64_t)u * BB;
-    uint32_t v[8];
-    ld_words_a2<8>(blk + 2, v);
-    const float d = h2f(ldu16(blk));
-    const float S = q8_words_dot(v, xs + 16 * u, 0.f);
-    const float X = xs16[2 * u] + xs16[2 * u + 1];
-    return d * (256.f * S - 384.f * X);            // sum((u-128) x)
+    Raw r;
+    ld_words_a2<8>(blk + 2, r.v);
+    r.d = ldu16(blk);
+    return r;
+  }
+  __device__ static float dot(const Raw& r, int, const uint32_t* xp, const float* xg) {
+    const float S = q8_words_dot(r.v, xp, 0.f);
+    return h2f(r.d) * (256.f * S - 384.f * (xg[0] + xg[1]));   // sum((u-128) x)
   }
 };
 
@@ -264,15 +332,16 @@ struct FQ80S {
       for (int b = 0; b < 4; ++b) w[4 * i + b] = d * (float)(int8_t)((v[i] >> (8 * b)) & 0xFF);
   }
 
-  __device__ static float unit_dot(const QArgs& a, int64_t n, int u, const uint32_t* xs,
-                                   const float* xs16) {
+  struct Raw { uint32_t v[8]; uint32_t d; };
+  __device__ static int run_start(int u, int) { return 32 * u; }
+  __device__ static Raw load(const QArgs& a, int64_t n, int u) {
     const uint8_t* q = a.w + n * a.rb + 32 * u;
     const u32x4 q0 = ld16(q), q1 = ld16(q + 16);
-    const uint32_t v[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    const float d = h2f(a.s[n * (a.K >> 5) + u]);
-    const float S = q8_words_dot(v, xs + 16 * u, 0.f);
-    const float X = xs16[2 * u] + xs16[2 * u + 1];
-    return d * (256.f * S - 384.f * X);
+    return Raw{{q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w}, a.s[n * (a.K >> 5) + u]};
+  }
+  __device__ static float dot(const Raw& r, int, const uint32_t* xp, const float* xg) {
+    const float S = q8_words_dot(r.v, xp, 0.f);
+    return h2f(r.d) * (256.f * S - 384.f * (xg[0] + xg[1]));
   }
 };
 
@@ -299,21 +368,26 @@ struct FQ50 {
     }
   }
 
-  __device__ static float unit_dot(const QArgs& a, int64_t n, int u, const uint32_t* xs,
-                                   const float* xs16) {
+  struct Raw { uint32_t qs[4], qh, d; };
+  __device__ static int run_start(int u, int) { return 32 * u; }
+  __device__ static Raw load(const QArgs& a, int64_t n, int u) {
     const uint8_t* blk = a.w + n * a.rb + (int64_t)u * BB;
-    uint32_t qh1[1], qs[4];
+    Raw r;
+    uint32_t qh1[1];
     ld_words_a2<1>(blk + 2, qh1);
-    ld_words_a2<4>(blk + 6, qs);
-    const uint32_t qh = qh1[0];
-    const float d = h2f(ldu16(blk));
-    const uint32_t* xp = xs + 16 * u;
+    ld_words_a2<4>(blk + 6, r.qs);
+    r.qh = qh1[0];
+    r.d = ldu16(blk);
+    return r;
+  }
+  __device__ static float dot(const Raw& r, int, const uint32_t* xp, const float* xg) {
+    const uint32_t qh = r.qh;
     float S = 0.f;
     // 5-bit u in fp16 mantissa bits 5..9 -> 1 + u/32; the 5th bits of elements
     // (l, l+2) are spread to bits 9 and 25 by (t & 5) * 0x00800200.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t v = qs[i];
+      const uint32_t v = r.qs[i];
       const int l = 4 * i;
       const uint32_t hA0 = (((qh >> l) & 5u) * 0x00800200u) & 0x02000200u;
       const uint32_t hA1 = (((qh >> (l + 1)) & 5u) * 0x00800200u) & 0x02000200u;
@@ -324,8 +398,7 @@ struct FQ50 {
       S = dot2(((v << 1) & 0x01E001E0u) | hB0 | MAGIC1, xp[8 + 2 * i], S);
       S = dot2(((v >> 7) & 0x01E001E0u) | hB1 | MAGIC1, xp[8 + 2 * i + 1], S);
     }
-    const float X = xs16[2 * u] + xs16[2 * u + 1];
-    return d * (32.f * S - 48.f * X);              // sum((u-16) x)
+    return h2f(r.d) * (32.f * S - 48.f * (xg[0] + xg[1]));     // sum((u-16) x)
   }
 };
 
@@ -348,24 +421,25 @@ struct FQ50S {
     }
   }
 
-  __device__ static float unit_dot(const QArgs& a, int64_t n, int u, const uint32_t* xs,
-                                   const float* xs16) {
+  struct Raw { u32x4 q, hq; uint32_t d; };
+  __device__ static int run_start(int u, int) { return 32 * u; }
+  __device__ static Raw load(const QArgs& a, int64_t n, int u) {
     const int64_t off = n * a.rb + 16 * u;
-    const u32x4 q = ld16(a.w + off), hq = ld16(a.aux + off);
-    const uint32_t qv[4] = {q.x, q.y, q.z, q.w}, hv[4] = {hq.x, hq.y, hq.z, hq.w};
-    const float d = h2f(a.s[n * (a.K >> 5) + u]);
-    const uint32_t* xp = xs + 16 * u;             // perm8 pairs
+    return Raw{ld16(a.w + off), ld16(a.aux + off), a.s[n * (a.K >> 5) + u]};
+  }
+  __device__ static float dot(const Raw& r, int, const uint32_t* xp, const float* xg) {
+    const uint32_t qv[4] = {r.q.x, r.q.y, r.q.z, r.q.w}, hv[4] = {r.hq.x, r.hq.y, r.hq.z, r.hq.w};
+    const uint32_t magic = MAGIC1;
     float S = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t v = qv[i], c = hv[i];
-      S = dot2(((v << 5) & 0x01E001E0u) | ((c << 9) & 0x02000200u) | MAGIC1, xp[4 * i], S);
-      S = dot2(((v >> 3) & 0x01E001E0u) | ((c << 1) & 0x02000200u) | MAGIC1, xp[4 * i + 1], S);
-      S = dot2(((v << 1) & 0x01E001E0u) | ((c << 5) & 0x02000200u) | MAGIC1, xp[4 * i + 2], S);
-      S = dot2(((v >> 7) & 0x01E001E0u) | ((c >> 3) & 0x02000200u) | MAGIC1, xp[4 * i + 3], S);
+      S = dot2(bfi(0x02000200u, c << 9, bfi(0x01E001E0u, v << 5, magic)), xp[4 * i], S);
+      S = dot2(bfi(0x02000200u, c << 1, bfi(0x01E001E0u, v >> 3, magic)), xp[4 * i + 1], S);
+      S = dot2(bfi(0x02000200u, c << 5, bfi(0x01E001E0u, v << 1, magic)), xp[4 * i + 2], S);
+      S = dot2(bfi(0x02000200u, c >> 3, bfi(0x01E001E0u, v >> 7, magic)), xp[4 * i + 3], S);
     }
-    const float X = xs16[2 * u] + xs16[2 * u + 1];
-    return d * (32.f * S - 48.f * X);
+    return h2f(r.d) * (32.f * S - 48.f * (xg[0] + xg[1]));
   }
 };
 
@@ -387,24 +461,26 @@ struct FMLX {
     }
   }
 
-  __device__ static float unit_dot(const QArgs& a, int64_t n, int u, const uint32_t* xs,
-                                   const float* xs16) {
-    const u32x4 q = ld16(a.w + n * a.rb + 16 * u);
-    const uint32_t v[4] = {q.x, q.y, q.z, q.w};
+  struct Raw { u32x4 q; uint32_t s, b; };
+  __device__ static int run_start(int u, int) { return 32 * u; }
+  __device__ static Raw load(const QArgs& a, int64_t n, int u) {
     const int64_t gi = n * (a.K / a.gs) + (32 * u) / a.gs;
-    const float s = h2f(a.s[gi]), b = h2f(a.b[gi]);
-    const uint32_t* xp = xs + 16 * u;             // perm8 pairs
+    return Raw{ld16(a.w + n * a.rb + 16 * u), a.s[gi], a.b[gi]};
+  }
+  __device__ static float dot(const Raw& r, int, const uint32_t* xp, const float* xg) {
+    const uint32_t v[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+    const uint32_t magic = MAGIC1;
     float S = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t v4 = v[i];
-      S = dot2(((v4 << 6) & 0x03C003C0u) | MAGIC1, xp[4 * i], S);       // (e0, e4)
-      S = dot2(((v4 >> 2) & 0x03C003C0u) | MAGIC1, xp[4 * i + 1], S);   // (e2, e6)
-      S = dot2(((v4 << 2) & 0x03C003C0u) | MAGIC1, xp[4 * i + 2], S);   // (e1, e5)
-      S = dot2(((v4 >> 6) & 0x03C003C0u) | MAGIC1, xp[4 * i + 3], S);   // (e3, e7)
+      uint32_t pr[4];
+      nib_pairs(v[i], magic, pr);                   // (e0,e4) (e2,e6) (e1,e5) (e3,e7)
+      S = dot2(pr[0], xp[4 * i], S);
+      S = dot2(pr[1], xp[4 * i + 1], S);
+      S = dot2(pr[2], xp[4 * i + 2], S);
+      S = dot2(pr[3], xp[4 * i + 3], S);
     }
-    const float X = xs16[2 * u] + xs16[2 * u + 1];
-    const float s16 = 16.f * s;
-    return s16 * S + (b - s16) * X;                // s sum(q x) + b X
+    const float s16 = 16.f * h2f(r.s);
+    return s16 * S + (h2f(r.b) - s16) * (xg[0] + xg[1]);           // s sum(q x) + b X
   }
 };

@@ -68,8 +68,10 @@ typedef enum {
  *     MLX_Q4:            w = qweight, scales, biases, group_size
  *     Q8_0_SPLIT:        w = qweight (int8), scales
  *     Q5_0_SPLIT:        w = qweight, aux = qhigh, scales
- *   `opts` packs launch knobs for tuning (0 = automatic): bits 0-7 lanes per
- *   row of the v_dot2 GEMV, bits 8-23 its grid cap, bits 24-27 MFMA GEMV row groups.
+ *   `opts` packs launch knobs for tuning (0 = automatic): bits 0-11 threads per
+ *   row of the v_dot2 GEMV (multiple of 16, 16..256), bits 12-27 its grid cap,
+ *   bits 28-31 MFMA GEMV row groups, bits 32-35 rows of weights in flight per
+ *   thread of the v_dot2 GEMV (2, 3 or 4).
  * No reference counterpart as a single op: the reference dispatches per format
  * (packages/alloy-torch/src/alloy_torch/ops/linalg.py:346-739); the named entry
  * points below are the per-op replacements and all route here.

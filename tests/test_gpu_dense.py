@@ -88,7 +88,7 @@ def test_gemv_dot2_m1(dev, fmt, N, K):
     y = wt.qmm(xt, path="gemv", out_dtype=torch.float32).cpu().numpy()
     check(y, x, wt.W, f"{fmt} gemv N={N} K={K}")
     # every lanes-per-row variant gives the same answer
-    for L in (4, 8, 16, 32, 64):
+    for L in (16, 32, 48, 64, 128, 256):
         yl = wt.qmm(xt, path="gemv", out_dtype=torch.float32, opts=L).cpu().numpy()
         check(yl, x, wt.W, f"{fmt} gemv L={L}")
 
@@ -115,7 +115,7 @@ def test_gemv_mfma(dev, fmt, M):
     x = synth.numpy_x(M, K, rng)
     xt = torch.from_numpy(x).to(dev)
     for rg in (1, 2):
-        y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=rg << 24).cpu().numpy()
+        y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=rg << 28).cpu().numpy()
         check(y, x, wt.W, f"{fmt} gemv_mfma M={M} rg={rg}")
 
 
