@@ -17,6 +17,7 @@ struct Opts {
   int grid_cap = 0;        // dot2 GEMV: max workgroups (grid-stride beyond)
   int row_groups = 0;      // MFMA GEMV: 16-row groups per workgroup (1, 2)
   int depth = 0;           // dot2 GEMV: rows of weights in flight per thread (2, 3, 4)
+  int variant = 0;         // dot2 GEMV: 0 automatic, 1 register ring, 2 LDS-staged tiles
 };
 
 hipError_t launch_dequant(int fmt, const QArgs& a, void* out, bool out_f16, int64_t row0,
@@ -30,6 +31,6 @@ hipError_t launch_gemm(int fmt, const QArgs& a, const void* x, bool x_f32, void*
 
 // The v_dot2 GEMV gives each thread at most 2 decode units of a 256-thread row:
 // K <= 512 units per row.
-inline int64_t max_k_dot2(int fmt) { return (fmt == F_Q4_K || fmt == F_Q6_K) ? 512 * 64 : 512 * 32; }
+inline int64_t max_k_dot2(int fmt) { return fmt == F_Q6_K ? 512 * 64 : 512 * 32; }
 
 }  // namespace alloy

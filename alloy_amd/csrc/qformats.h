@@ -14,8 +14,8 @@
 //                            (products exact, fp32 accumulation); the 1.0 bias is
 //                            removed with the per-16-element x sums xs16.  xr holds
 //                            the unit's x as fp16 pairs in the format's XPERM order,
-//                            one 32-element run after the other (run_start gives
-//                            the first element of each run).
+//                            one RUN-element run after the other (run_start gives
+//                            the first element of each run); xs16 its sums per 16.
 //   constants QK (block elements), UE (unit elements), XPERM (4 or 8).
 //
 // Layout citations (reference, read-only):
@@ -145,7 +145,8 @@ struct Q4kSel {
 };
 
 struct FQ4K {
-  static constexpr int QK = 256, BB = 144, UE = 64, XPERM = 4;
+  static constexpr int QK = 256, BB = 144, UE = 32, XPERM = 4;
+  static constexpr bool kStaged = true;   // rows live in one blob (LDS-staged GEMV)
 
   __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
     const uint8_t* blk = a.w + n * a.rb + (int64_t)(k0 >> 8) * BB;
@@ -167,23 +168,31 @@ struct FQ4K {
   }
 
   // unit u = (superblock u/4, pair p = u%4): sub-blocks 2p (low nibbles) and 2p+1.
-  // unit u = (superblock u/4, pair p = u%4): sub-blocks 2p (low nibbles) and 2p+1;
-  // runs: elements 64u + [0,32) and 64u + 32 + [0,32).
-  struct Raw { u32x4 h, q0, q1; };
-  __device__ static int run_start(int u, int r) { return 64 * u + 32 * r; }
-  __device__ static Raw load(const QArgs& a, int64_t n, int u) {
-    const uint8_t* blk = a.w + n * a.rb + (int64_t)(u >> 2) * BB;
-    const int p = u & 3;
-    return Raw{ld16(blk), ld16(blk + 16 + 32 * p), ld16(blk + 32 + 32 * p)};
+  // unit u = (superblock u/8, quant chunk c = u%8): the 16 bytes qs[16c, 16c+16),
+  // i.e. elements l0..l0+15 (l0 = 16*(c%2)) of sub-blocks 2p (low nibbles) and
+  // 2p+1 (high nibbles), p = c/2.  Eight consecutive lanes read the eight chunks
+  // of one superblock, so each load instruction covers contiguous 128-byte runs.
+  // runs (16 elements): 64p + l0 + [0,16) and 64p + 32 + l0 + [0,16).
+  static constexpr int RUN = 16;
+  struct Raw { u32x4 h, q; };
+  __device__ static int run_start(int u, int r) {
+    const int c = u & 7;
+    return 256 * (u >> 3) + 64 * (c >> 1) + 16 * (c & 1) + 32 * r;
+  }
+  __device__ static Raw load(const QArgs& a, int64_t n, int u) { return load_row(a.w + n * a.rb, u); }
+  // row: the row's bytes (global memory or an LDS tile)
+  __device__ static Raw load_row(const uint8_t* row, int u) {
+    const uint8_t* blk = row + (u >> 3) * BB;
+    return Raw{ld16(blk), ld16(blk + 16 + 16 * (u & 7))};
   }
   __device__ static float dot(const Raw& r, int u, const uint32_t* xa, const float* xg) {
-    const int p = u & 3;
-    const uint32_t words[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
-    const uint32_t* xb = xa + 16;                // sub-block B pairs
+    const int p = (u & 7) >> 1;
+    const uint32_t words[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+    const uint32_t* xb = xa + 8;                 // sub-block B pairs
     const uint32_t magic = MAGIC1;
     float SA = 0.f, SB = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4; ++i) {
       uint32_t pr[4];
       nib_pairs(words[i], magic, pr);
       SA = dot2(pr[0], xa[2 * i], SA);
@@ -191,14 +200,13 @@ struct FQ4K {
       SB = dot2(pr[2], xb[2 * i], SB);
       SB = dot2(pr[3], xb[2 * i + 1], SB);
     }
-    const float XA = xg[0] + xg[1], XB = xg[2] + xg[3];
     const float d16 = 16.f * h2f(r.h.x), dmin = h2f(r.h.x >> 16);
     uint32_t scA, mA, scB, mB;
     Q4kSel(2 * p).get(r.h.y, r.h.z, r.h.w, scA, mA);
     Q4kSel(2 * p + 1).get(r.h.y, r.h.z, r.h.w, scB, mB);
     const float cA = d16 * (float)scA, cB = d16 * (float)scB;
     // sum(q x) = 16 (S - X);  w = d sc q - dmin m
-    return cA * SA - (cA + dmin * (float)mA) * XA + cB * SB - (cB + dmin * (float)mB) * XB;
+    return cA * SA - (cA + dmin * (float)mA) * xg[0] + cB * SB - (cB + dmin * (float)mB) * xg[1];
   }
 };
 
@@ -208,6 +216,8 @@ struct FQ4K {
 // q = (nib | qh2<<4) - 32, scale 8h+2s+l/16; w = d*sc*q.
 struct FQ6K {
   static constexpr int QK = 256, BB = 210, UE = 64, XPERM = 4;
+  static constexpr int RUN = 32;        // x run length (elements) of a unit
+  static constexpr bool kStaged = true;   // rows live in one blob (LDS-staged GEMV)
 
   __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
     const uint8_t* blk = a.w + n * a.rb + (int64_t)(k0 >> 8) * BB;
@@ -236,9 +246,10 @@ struct FQ6K {
   __device__ static int run_start(int u, int r) {
     return 256 * (u >> 2) + 128 * ((u >> 1) & 1) + 32 * (u & 1) + 64 * r;
   }
-  __device__ static Raw load(const QArgs& a, int64_t n, int u) {
+  __device__ static Raw load(const QArgs& a, int64_t n, int u) { return load_row(a.w + n * a.rb, u); }
+  __device__ static Raw load_row(const uint8_t* row, int u) {
     const int h = (u >> 1) & 1, s0 = u & 1;
-    const uint8_t* blk = a.w + n * a.rb + (int64_t)(u >> 2) * BB;
+    const uint8_t* blk = row + (u >> 2) * BB;
     Raw r;
     ld_words_a2<8>(blk + 64 * h + 32 * s0, r.ql);
     ld_words_a2<8>(blk + 128 + 32 * h, r.qh);
@@ -290,6 +301,8 @@ __device__ __forceinline__ float q8_words_dot(const uint32_t (&v)[8], const uint
 
 struct FQ80 {
   static constexpr int QK = 32, BB = 34, UE = 32, XPERM = 4;
+  static constexpr int RUN = 32;        // x run length (elements) of a unit
+  static constexpr bool kStaged = true;   // rows live in one blob (LDS-staged GEMV)
 
   __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
     const uint8_t* blk = a.w + n * a.rb + (int64_t)(k0 >> 5) * BB;
@@ -304,8 +317,9 @@ struct FQ80 {
 
   struct Raw { uint32_t v[8]; uint32_t d; };
   __device__ static int run_start(int u, int) { return 32 * u; }
-  __device__ static Raw load(const QArgs& a, int64_t n, int u) {
-    const uint8_t* blk = a.w + n * a.rb + (int64_t)u * BB;
+  __device__ static Raw load(const QArgs& a, int64_t n, int u) { return load_row(a.w + n * a.rb, u); }
+  __device__ static Raw load_row(const uint8_t* row, int u) {
+    const uint8_t* blk = row + u * BB;
     Raw r;
     ld_words_a2<8>(blk + 2, r.v);
     r.d = ldu16(blk);
@@ -320,6 +334,8 @@ struct FQ80 {
 // Q8_0 split layout (reference loader): qweight int8[N,K], scales fp16[N,K/32].
 struct FQ80S {
   static constexpr int QK = 32, BB = 32, UE = 32, XPERM = 4;
+  static constexpr int RUN = 32;        // x run length (elements) of a unit
+  static constexpr bool kStaged = false;   // rows live in one blob (LDS-staged GEMV)
 
   __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
     const uint8_t* q = a.w + n * a.rb + k0;
@@ -350,6 +366,8 @@ struct FQ80S {
 // element l+16: (qs[l]>>4) | bit_{l+16}(qh)<<4; w = (q-16)*d.
 struct FQ50 {
   static constexpr int QK = 32, BB = 22, UE = 32, XPERM = 4;
+  static constexpr int RUN = 32;        // x run length (elements) of a unit
+  static constexpr bool kStaged = true;   // rows live in one blob (LDS-staged GEMV)
 
   __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
     const uint8_t* blk = a.w + n * a.rb + (int64_t)(k0 >> 5) * BB;
@@ -370,8 +388,9 @@ struct FQ50 {
 
   struct Raw { uint32_t qs[4], qh, d; };
   __device__ static int run_start(int u, int) { return 32 * u; }
-  __device__ static Raw load(const QArgs& a, int64_t n, int u) {
-    const uint8_t* blk = a.w + n * a.rb + (int64_t)u * BB;
+  __device__ static Raw load(const QArgs& a, int64_t n, int u) { return load_row(a.w + n * a.rb, u); }
+  __device__ static Raw load_row(const uint8_t* row, int u) {
+    const uint8_t* blk = row + u * BB;
     Raw r;
     uint32_t qh1[1];
     ld_words_a2<1>(blk + 2, qh1);
@@ -407,6 +426,8 @@ struct FQ50 {
 // scales fp16[N,K/32].  packages/alloy-metal/src/alloy/std/quant.py:1025-1034.
 struct FQ50S {
   static constexpr int QK = 32, BB = 16, UE = 32, XPERM = 8;
+  static constexpr int RUN = 32;        // x run length (elements) of a unit
+  static constexpr bool kStaged = false;   // rows live in one blob (LDS-staged GEMV)
 
   __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
     const int64_t off = n * a.rb + (k0 >> 1);
@@ -448,6 +469,8 @@ struct FQ50S {
 // fp16[N,K/gs]; w = s*q + b.  Units of 32 elements require gs % 32 == 0.
 struct FMLX {
   static constexpr int QK = 32, BB = 16, UE = 32, XPERM = 8;
+  static constexpr int RUN = 32;        // x run length (elements) of a unit
+  static constexpr bool kStaged = false;   // rows live in one blob (LDS-staged GEMV)
 
   __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
     const u32x4 q = ld16(a.w + n * a.rb + (k0 >> 1));
