@@ -7,8 +7,10 @@
 //                   (order within an expert = route order), inverse permutation, and
 //                   a list of column tiles (<= 16 routes of one expert each)
 //                   (reference role: moe.py:504-735, without padding rows)
-//   3. k_gate_up    per (tile, 16 gate rows): gathered MFMA GEMV over the tile's
-//                   tokens, h = silu(G_e x) * (U_e x) stored fp16 per sorted route
+//   3. k_gate_up    per (tile, 16 gate rows): gathered exact MFMA GEMV over the
+//                   tile's tokens (quants as fp16 integers, group scale and bias
+//                   applied in fp32), h = silu(G_e x) * (U_e x) stored fp16 per
+//                   sorted route
 //                   (reference role: moe.py:82-135, 225-306; fused rows [0:I] gate,
 //                   [I:2I] up, packages/alloy-server/src/alloy_server/models/qwen3_5.py:383-385)
 //   4. k_down       per (tile, 16 hidden rows): D_e h -> fp32 partial per sorted route
@@ -227,6 +229,56 @@ __device__ __forceinline__ void reduce_waves(f32x4 (&acc)[NA], float (*red)[NA][
         for (int t = 0; t < 4; ++t) acc[a][t] += red[w][a][lane][t];
 }
 
+// Exact grouped MFMA over MLX rows.  A = 16 activation rows (lane % 16), B = 16
+// weight rows (lane % 16) whose quants enter as the fp16 integers 1024 + q (exact:
+// the nibble is OR-ed into the mantissa of 1024.0), so every product is exact and
+// the MFMA sums them in fp32.  Per group g (gs elements, a multiple of 32) with a
+// fresh accumulator:  sum_k w x = s*sum q x + b*X = s*D + (b - 1024 s)*X, where
+// D = sum (1024 + q) x and X = sum x (the same MFMA against a ones operand).  The
+// activations are permuted to the nibble order (e0,e4)(e1,e5)(e2,e6)(e3,e7) that the
+// unpack produces.  Groups are dealt round-robin to the 4 waves.
+// Result: acc[w][t] = partial of activation row 4*(lane/16)+t times weight row lane%16.
+#define MAGIC1024 0x64006400u   // fp16 1024.0 in both halves
+
+template <int NW>
+__device__ __forceinline__ void mlx_rows_mfma(const QArgs& a, const int64_t (&row)[NW], bool rin,
+                                              const f16* act, bool ain, f32x4 (&acc)[NW]) {
+  const int K = a.K, gs = a.gs, G = K / gs;
+  const int wave = threadIdx.x >> 6, kq = (threadIdx.x & 63) >> 4;
+  const f16x8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+  const uint32_t magic = MAGIC1024;
+  for (int g = wave; g < G; g += 4) {
+    f32x4 dX = {0.f, 0.f, 0.f, 0.f};
+    f32x4 dW[NW];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) dW[w] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int h = 0; h < gs; h += 32) {
+      const int k = g * gs + h + 8 * kq;
+      u32x4 xv = ain ? *(const u32x4*)(act + k) : u32x4{0u, 0u, 0u, 0u};
+      // (x0,x4) (x1,x5) (x2,x6) (x3,x7)
+      const u32x4 xp = {__builtin_amdgcn_perm(xv.z, xv.x, 0x05040100u), __builtin_amdgcn_perm(xv.z, xv.x, 0x07060302u),
+                        __builtin_amdgcn_perm(xv.w, xv.y, 0x05040100u), __builtin_amdgcn_perm(xv.w, xv.y, 0x07060302u)};
+      const f16x8 af = __builtin_bit_cast(f16x8, xp);
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const uint32_t q = rin ? *(const uint32_t*)(a.w + row[w] * a.rb + (k >> 1)) : 0u;
+        const u32x4 bq = {bfi(0x000F000Fu, q, magic), bfi(0x000F000Fu, q >> 4, magic),
+                          bfi(0x000F000Fu, q >> 8, magic), bfi(0x000F000Fu, q >> 12, magic)};
+        dW[w] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, __builtin_bit_cast(f16x8, bq), dW[w], 0, 0, 0);
+      }
+      dX = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, ones, dX, 0, 0, 0);
+    }
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const int64_t gi = row[w] * G + g;
+      const float sc = rin ? h2f(a.s[gi]) : 0.f, bi = rin ? h2f(a.b[gi]) : 0.f;
+      const float c = bi - 1024.f * sc;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[w][t] += sc * dW[w][t] + c * dX[t];
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void k_gate_up(QArgs gu, const f16* x, const int32_t* sorted,
                                                  const int32_t* tiles, const int32_t* ntiles,
                                                  f16* h, int top_k, int I) {
@@ -237,39 +289,23 @@ __global__ __launch_bounds__(256) void k_gate_up(QArgs gu, const f16* x, const i
   const int i0 = blockIdx.y * 16;
   const int K = gu.K;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int i = lane & 15, kq = lane >> 4;
-  const int64_t tok = i < cnt ? (int64_t)(sorted[p0 + i] / top_k) : -1;
-  const bool rin = i0 + i < I;
-  const int64_t rowg = (int64_t)e * 2 * I + i0 + i, rowu = rowg + I;
+  const int n = lane & 15, kq = lane >> 4;
+  // A operand: routed token of column slot n; B operand: gate / up row i0 + n
+  const bool ain = n < cnt;
+  const f16* act = x + (ain ? (int64_t)(sorted[p0 + n] / top_k) * K : 0);
+  const bool rin = i0 + n < I;
+  const int64_t rg = (int64_t)e * 2 * I + (rin ? i0 + n : 0);
+  const int64_t row[2] = {rg, rg + I};
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-  for (int k0 = 128 * wave; k0 < K; k0 += 512) {
-    const int kk = k0 + 32 * kq;
-    const bool kin = kk < K;
-    f16x8 bfr[4], ag[4], au[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      bfr[j] = (kin && tok >= 0) ? *(const f16x8*)(x + tok * K + kk + 8 * j) : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    if (kin && rin) {
-      dec32_mlx_f16(gu, rowg, kk, ag);
-      dec32_mlx_f16(gu, rowu, kk, au);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) ag[j] = au[j] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ag[j], bfr[j], acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(au[j], bfr[j], acc[1], 0, 0, 0);
-    }
-  }
+  mlx_rows_mfma<2>(gu, row, rin, act, ain, acc);
   reduce_waves<2>(acc, red);
-  if (wave == 0 && i < cnt) {
+  if (wave == 0 && rin) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const int r = i0 + 4 * kq + t;
-      if (r < I) {
+      const int m = 4 * kq + t;                 // route slot within the tile
+      if (m < cnt) {
         const float g = acc[0][t], u = acc[1][t];
-        h[(int64_t)(p0 + i) * I + r] = (f16)(g / (1.f + expf(-g)) * u);
+        h[(int64_t)(p0 + m) * I + i0 + n] = (f16)(g / (1.f + expf(-g)) * u);
       }
     }
   }
@@ -284,32 +320,19 @@ __global__ __launch_bounds__(256) void k_down(QArgs dn, const f16* h, const int3
   const int j0 = blockIdx.y * 16;
   const int K = dn.K;   // = I
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int i = lane & 15, kq = lane >> 4;
-  const bool cin = i < cnt;
-  const bool rin = j0 + i < H;
-  const int64_t row = (int64_t)e * H + j0 + i;
+  const int n = lane & 15, kq = lane >> 4;
+  const bool ain = n < cnt;
+  const f16* act = h + (ain ? (int64_t)(p0 + n) * K : 0);
+  const bool rin = j0 + n < H;
+  const int64_t row[1] = {(int64_t)e * H + (rin ? j0 + n : 0)};
   f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
-  for (int k0 = 128 * wave; k0 < K; k0 += 512) {
-    const int kk = k0 + 32 * kq;
-    const bool kin = kk < K;
-    f16x8 bfr[4], af[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      bfr[j] = (kin && cin) ? *(const f16x8*)(h + (int64_t)(p0 + i) * K + kk + 8 * j) : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    if (kin && rin) dec32_mlx_f16(dn, row, kk, af);
-    else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) af[j] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[j], bfr[j], acc[0], 0, 0, 0);
-  }
+  mlx_rows_mfma<1>(dn, row, rin, act, ain, acc);
   reduce_waves<1>(acc, red);
-  if (wave == 0 && cin) {
+  if (wave == 0 && rin) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const int r = j0 + 4 * kq + t;
-      if (r < H) part[(int64_t)(p0 + i) * H + r] = acc[0][t];
+      const int m = 4 * kq + t;
+      if (m < cnt) part[(int64_t)(p0 + m) * H + j0 + n] = acc[0][t];
     }
   }
 }

@@ -196,14 +196,31 @@ def prefill_gemm(dev, qmm, M=2048, reps=10):
 
 
 def traffic_from_profiles():
-    """HBM bytes per launch of the dominant kernel, from the committed PMC summary."""
-    p = ROOT / "profiles" / "q4k_gemv_decode_pmc.json"
-    if not p.exists():
-        return None
+    """HBM bytes per launch of the dominant kernel, from the committed PMC summary
+    (a line ``traffic_bytes_per_launch = N`` in profiles/q4k_gemv_decode_pmc.md)."""
+    import re
+
+    p = ROOT / "profiles" / "q4k_gemv_decode_pmc.md"
     try:
-        return json.loads(p.read_text()).get("hbm_bytes_per_launch")
-    except (OSError, ValueError):
+        m = re.search(r"^traffic_bytes_per_launch = (\d+)", p.read_text(), re.M)
+    except OSError:
         return None
+    return int(m.group(1)) if m else None
+
+
+def copy_calibration(dev, mib=256, reps=5):
+    """A plain device copy of known size (torch's copy kernel), for scaling the
+    FETCH_SIZE / WRITE_SIZE counters: each launch reads and writes mib MiB."""
+    import torch
+
+    a = torch.empty(mib << 20, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    a.fill_(1)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_per_launch": mib << 20, "launches": reps}))
 
 
 def main():
@@ -213,6 +230,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="time the decode step only (no per-shape, prefill or CPU legs)")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch the decode step eagerly instead of replaying a HIP graph (counter runs)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a 256 MiB device copy (counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -225,16 +248,34 @@ def main():
     from alloy_amd import qmm
 
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        copy_calibration(dev)
+        return
     alloy_amd.lib()
     log("building decode step weights ...")
     mats, xs, ys = build_decode_step(dev)
     total_bytes = sum(q4k_bytes(K, N) for _, K, N, _ in mats)
     stream = torch.cuda.current_stream(dev)
-    log(f"{len(mats)} GEMVs, {total_bytes} weight bytes; capturing the step as a HIP graph")
-    graph = capture(lambda: run_step(mats, xs, ys, qmm), dev)
-    t = time_replays(graph, args.steps, args.warmup, stream)
+    if args.eager:
+        log(f"{len(mats)} GEMVs, {total_bytes} weight bytes; eager launches")
+        for _ in range(args.warmup):
+            run_step(mats, xs, ys, qmm)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            run_step(mats, xs, ys, qmm)
+        torch.cuda.synchronize()
+        t = time.perf_counter() - t0
+    else:
+        log(f"{len(mats)} GEMVs, {total_bytes} weight bytes; capturing the step as a HIP graph")
+        graph = capture(lambda: run_step(mats, xs, ys, qmm), dev)
+        t = time_replays(graph, args.steps, args.warmup, stream)
     ms = t / args.steps * 1e3
     value = total_bytes * args.steps / t / 1e9
+    if args.decode_only:
+        print(json.dumps({"decode_step_ms": round(ms, 4), "weight_GBps": round(value, 2),
+                          "eager": args.eager, "steps": args.steps}))
+        return
 
     per = per_shape_times(mats, xs, ys, qmm, dev)
     counts = {}
