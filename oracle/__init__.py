@@ -15,7 +15,7 @@ Modules
 Parity pinning (how each function is checked, beyond retyping it):
 
 * every decoder: known-answer blocks whose expected values are written out by
-  hand in ``tests/test_oracle_kat.py``, plus an independent element-by-element
+  hand in ``tests/test_oracle.py``, plus an independent element-by-element
   ENCODER (``tests/golden/make_golden.py``) whose round trip
   encode(params) -> decode == d*sc*q - dmin*m is checked on random parameters
   (committed fixtures ``tests/golden/*.npz``), plus the fp32 exactness lemma
