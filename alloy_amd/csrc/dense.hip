@@ -89,13 +89,6 @@ __device__ __forceinline__ void load_x_unit(const XT* x, int u, uint32_t (&xr)[F
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[8 * c + e] = t[e];
     }
-#pragma unroll
-    for (int h = 0; h < RUN / 16; ++h) {
-      float sum = 0.f;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) sum += (float)v[16 * h + e];
-      xg[(RUN / 16) * r + h] = sum;
-    }
     uint32_t* o = xr + (RUN / 2) * r;
     if (F::XPERM == 4) {
 #pragma unroll
@@ -112,6 +105,15 @@ __device__ __forceinline__ void load_x_unit(const XT* x, int u, uint32_t (&xr)[F
         o[4 * j + 2] = pack2(v[b + 1], v[b + 5]);
         o[4 * j + 3] = pack2(v[b + 3], v[b + 7]);
       }
+    }
+    // per-16-element sums: pairs 8h..8h+7 hold exactly elements 16h..16h+15 in
+    // either order; v_dot2 against (1, 1) adds them in fp32 without conversions
+#pragma unroll
+    for (int h = 0; h < RUN / 16; ++h) {
+      float sum = 0.f;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) sum = dot2(o[8 * h + q], MAGIC1, sum);
+      xg[(RUN / 16) * r + h] = sum;
     }
   }
 }
@@ -188,6 +190,98 @@ __global__ __launch_bounds__(256) void k_gemv_dot2(QArgs a, const XT* x, void* y
       const float v = step(d, n);
       if (li == 0 && n < N) store_y(y, y_f32, m * N + n, v);
     }
+  }
+}
+
+// ------------------------------------------------------------------ M=1 GEMV, wave rows
+// L = 16, 32 or 64 lanes share a row inside one wave (64/L rows per wave, 256/L per
+// workgroup); each lane owns UPT decode units of the row, the same for every row
+// it visits, with their x in registers.  Weights stream through a ring of D rows
+// per lane by raw buffer loads: offsets are 32-bit, and rows past N read as zero
+// (no clamps, no faults), so every refill is unconditional.  A row's partial sums
+// reduce across its L lanes with DPP (quad_perm, row mirrors, row_bcast 15/31) —
+// no LDS, no barrier — and the row's last lane stores it.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROW_MASK, 0xF, false));
+}
+// Sum over groups of 1 << lshift lanes (16, 32 or 64); the total is complete in the
+// group's last lane.  Branch-free in lshift, so the loop body has no control flow.
+__device__ __forceinline__ float dpp_sum_rows(float v, int lshift) {
+  v += dpp_f<0xB1, 0xF>(v);     // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E, 0xF>(v);     // quad_perm [2,3,0,1]
+  v += dpp_f<0x141, 0xF>(v);    // row_half_mirror: 8-lane sums
+  v += dpp_f<0x140, 0xF>(v);    // row_mirror: every lane of a 16-lane row holds its sum
+  const float s32 = v + dpp_f<0x142, 0xA>(v);        // row_bcast:15 -> rows 1, 3: 32-lane sums
+  const float s64 = s32 + dpp_f<0x143, 0xC>(s32);    // row_bcast:31 -> row 3: 64-lane sum
+  return lshift == 4 ? v : lshift == 5 ? s32 : s64;
+}
+
+template <class F, int UPT, int D, typename XT, typename YT>
+__global__ __launch_bounds__(256) void k_gemv_w(QArgs a, uint32_t sb, const XT* x, YT* y,
+                                                int64_t ldy, int N, int lshift) {
+  const int L = 1 << lshift;
+  const int t = threadIdx.x, li = t & (L - 1), slot = t >> lshift;
+  const int R = blockDim.x >> lshift;
+  const int K = a.K, U = K / F::UE;
+  const int64_t m = blockIdx.y;
+  const uint32_t rb = (uint32_t)a.rb;
+  const Src src(a, (uint32_t)N * rb, (uint32_t)N * sb);
+  // output row m as a buffer: every lane stores, lanes other than a group's last one
+  // (and rows >= N) aim past the end, so the hardware drops them — no branch
+  constexpr uint32_t esz = sizeof(YT);
+  const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(y + m * ldy), (short)0, (int)((uint32_t)N * esz), ALLOY_RSRC_DW3);
+  bool own[UPT];
+  int uu[UPT];
+  uint32_t wo[UPT], so[UPT];
+#pragma unroll
+  for (int j = 0; j < UPT; ++j) {
+    const int u = li + L * j;
+    own[j] = u < U;
+    uu[j] = own[j] ? u : U - 1;            // x and decode of a valid unit; result dropped
+    wo[j] = F::woff(a, uu[j]);
+    so[j] = F::soff(a, uu[j]);
+  }
+  const int stride = (int)gridDim.x * R;
+  const int n0 = (int)blockIdx.x * R + slot;
+  uint32_t rw = (uint32_t)n0 * rb, rs = (uint32_t)n0 * sb;   // row offsets of ring slot 0
+  const uint32_t dw = (uint32_t)stride * rb, ds = (uint32_t)stride * sb;
+  typename F::Raw ring[D][UPT];
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+#pragma unroll
+    for (int j = 0; j < UPT; ++j) ring[d][j] = F::load_b(src, rw + d * dw + wo[j], rs + d * ds + so[j], uu[j]);
+  uint32_t xr[UPT][F::UE / 2];
+  float xg[UPT][F::UE / 16];
+  const XT* xm = x + m * K;
+#pragma unroll
+  for (int j = 0; j < UPT; ++j) load_x_unit<F, XT>(xm, uu[j], xr[j], xg[j]);
+
+  for (int base = (int)blockIdx.x * R; base < N; base += D * stride) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int nb = base + d * stride;      // uniform across the workgroup
+      // leave the kernel, not just the unrolled steps: a jump to the loop latch would
+      // merge a state with only some slots refilled into the loop head and force a
+      // full vmcnt wait there
+      if (nb >= N) return;
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < UPT; ++j) {
+        const float v = F::dot(ring[d][j], uu[j], xr[j], xg[j]);
+        acc += own[j] ? v : 0.f;
+      }
+      const uint32_t nw = rw + (d + D) * dw, ns = rs + (d + D) * ds;
+#pragma unroll
+      for (int j = 0; j < UPT; ++j) ring[d][j] = F::load_b(src, nw + wo[j], ns + so[j], uu[j]);
+      acc = dpp_sum_rows(acc, lshift);
+      const uint32_t yo = li == L - 1 ? (uint32_t)(nb + slot) * esz : 0x80000000u;
+      if constexpr (sizeof(YT) == 4) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc), yr, yo, 0, 0);
+      else __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (f16)acc), yr, yo, 0, 0);
+    }
+    rw += D * dw;
+    rs += D * ds;
   }
 }
 
@@ -537,9 +631,84 @@ struct GemvDot2Run {
   }
 };
 
+// Wave-row GEMV launcher.  Returns hipErrorNotSupported when the shape needs more
+// than 4 units per lane at 64 lanes per row (then the LDS-combining kernel runs).
+template <class F>
+struct GemvWaveRun {
+  template <int UPT, int D, typename YT>
+  static hipError_t go(const QArgs& a, uint32_t sb, const void* x, void* y, int64_t ldy, int64_t M,
+                       int64_t N, int lshift, int grid_cap, hipStream_t st) {
+    const int R = 256 >> lshift;
+    int64_t grid = (N + R - 1) / R;
+    const int64_t cap = grid_cap > 0 ? grid_cap : 1024;
+    if (grid > cap) grid = cap;
+    hipLaunchKernelGGL((k_gemv_w<F, UPT, D, f16, YT>), dim3((unsigned)grid, (unsigned)M), dim3(256), 0, st,
+                       a, sb, (const f16*)x, (YT*)y, ldy, (int)N, lshift);
+    return hipGetLastError();
+  }
+  template <int UPT, typename YT>
+  static hipError_t pick_d(int depth, const QArgs& a, uint32_t sb, const void* x, void* y, int64_t ldy,
+                           int64_t M, int64_t N, int lshift, int cap, hipStream_t st) {
+    if (depth == 1) return go<UPT, 1, YT>(a, sb, x, y, ldy, M, N, lshift, cap, st);
+    return go<UPT, 2, YT>(a, sb, x, y, ldy, M, N, lshift, cap, st);
+  }
+  template <typename YT>
+  static hipError_t pick(int upt, int depth, const QArgs& a, uint32_t sb, const void* x, void* y,
+                         int64_t ldy, int64_t M, int64_t N, int lshift, int cap, hipStream_t st) {
+    switch (upt) {
+      case 1: return pick_d<1, YT>(depth, a, sb, x, y, ldy, M, N, lshift, cap, st);
+      case 2: return pick_d<2, YT>(depth, a, sb, x, y, ldy, M, N, lshift, cap, st);
+      case 3: return pick_d<3, YT>(depth, a, sb, x, y, ldy, M, N, lshift, cap, st);
+      default: return pick_d<4, YT>(depth, a, sb, x, y, ldy, M, N, lshift, cap, st);
+    }
+  }
+  static hipError_t run(const QArgs& a, uint32_t sb, const void* x, bool x_f32, void* y, int64_t ldy,
+                        bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st) {
+    if (x_f32) return hipErrorNotSupported;         // fp32 activations: ring kernel
+    const int U = a.K / F::UE;
+    int lshift;
+    if (o.lanes_per_row == 16 || o.lanes_per_row == 32 || o.lanes_per_row == 64)
+      lshift = o.lanes_per_row == 16 ? 4 : o.lanes_per_row == 32 ? 5 : 6;
+    else {
+      lshift = U <= 64 ? 4 : U <= 128 ? 5 : 6;          // at most 4 units per lane
+      // short matrices: more lanes per row until there are >= 512 workgroups
+      while (lshift < 6 && (N << lshift) < 512 * 256) ++lshift;
+    }
+    const int L = 1 << lshift;
+    const int upt = (U + L - 1) / L;
+    if (upt > 4) return hipErrorNotSupported;
+    // one row in flight per lane, latency hidden by occupancy: measured at least as
+    // fast as a two-row register ring on every decode shape
+    const int depth = o.depth == 2 ? 2 : 1;
+    const int cap = o.grid_cap > 0 ? o.grid_cap : (N > 32768 ? 1024 : 512);
+    return y_f32 ? pick<float>(upt, depth, a, sb, x, y, ldy, M, N, lshift, cap, st)
+                 : pick<f16>(upt, depth, a, sb, x, y, ldy, M, N, lshift, cap, st);
+  }
+};
+
 hipError_t launch_gemv_dot2(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
                             bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;
+  if (o.variant == 0 || o.variant == 3) {
+    // scale-row bytes (MLX scales/biases, split-layout scales) for the buffer views
+    const uint32_t sb = fmt == F_MLX ? (uint32_t)(2 * (a.K / a.gs))
+                      : (fmt == F_Q8_0S || fmt == F_Q5_0S) ? (uint32_t)(2 * (a.K / 32)) : 0u;
+    // 32-bit buffer offsets: split the rows into ranges below 2 GiB of weights
+    const int64_t wrow = a.rb > 0 ? a.rb : 1;
+    const int64_t rows = ((int64_t)1 << 31) / (wrow > (int64_t)sb ? wrow : (int64_t)sb) - 1024;
+    hipError_t e = hipSuccess;
+    for (int64_t r0 = 0; r0 < N && e == hipSuccess; r0 += rows) {
+      const int64_t nr = N - r0 < rows ? N - r0 : rows;
+      QArgs ar = a;
+      ar.w = a.w + r0 * a.rb;
+      if (a.aux) ar.aux = a.aux + r0 * a.rb;
+      if (a.s) ar.s = a.s + r0 * (sb / 2);
+      if (a.b) ar.b = a.b + r0 * (sb / 2);
+      e = by_fmt<GemvWaveRun>(fmt, ar, sb, x, x_f32, (uint8_t*)y + r0 * (y_f32 ? 4 : 2), (int64_t)N, y_f32, M, nr, o, st);
+    }
+    if (e != hipErrorNotSupported) return e;
+    (void)hipGetLastError();
+  }
   return by_fmt<GemvDot2Run>(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
 }
 

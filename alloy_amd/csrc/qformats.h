@@ -95,6 +95,43 @@ __device__ __forceinline__ uint32_t lshl_or(uint32_t a, uint32_t b) {           
   return r;
 }
 
+// Buffer-resource view of one weight matrix (w, aux, s, b), for the streaming
+// GEMV.  Raw buffer loads check the offset against the resource size and return
+// zero past the end, so rows beyond N (the prefetch runs ahead of the last row)
+// need no clamping and can never fault.  Offsets are 32-bit: the host splits
+// matrices of 2 GiB or more into row ranges.
+#define ALLOY_RSRC_DW3 0x00020000   // gfx9 buffer descriptor word 3: 32-bit data format
+struct Src {
+  __amdgpu_buffer_rsrc_t w, aux, s, b;
+  __device__ Src(const QArgs& a, uint32_t wbytes, uint32_t sbytes) {
+    w = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, (int)wbytes, ALLOY_RSRC_DW3);
+    aux = __builtin_amdgcn_make_buffer_rsrc((void*)a.aux, (short)0, a.aux ? (int)wbytes : 0, ALLOY_RSRC_DW3);
+    s = __builtin_amdgcn_make_buffer_rsrc((void*)a.s, (short)0, a.s ? (int)sbytes : 0, ALLOY_RSRC_DW3);
+    b = __builtin_amdgcn_make_buffer_rsrc((void*)a.b, (short)0, a.b ? (int)sbytes : 0, ALLOY_RSRC_DW3);
+  }
+};
+__device__ __forceinline__ u32x4 bld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bld2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+// NW little-endian words at a 2-byte-aligned offset: aligned dword loads plus one
+// u16 load, merged with v_alignbyte (same bytes as ld_words_a2).
+template <int NW>
+__device__ __forceinline__ void bwords_a2(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t (&o)[NW]) {
+  const uint32_t sh = off & 2u, base = off - sh;
+  uint32_t t[NW + 1];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) t[i] = bld4(r, base + 4 * i);
+  t[NW] = bld2(r, off + 4 * NW - 2);
+#pragma unroll
+  for (int i = 0; i < NW; ++i) o[i] = __builtin_amdgcn_alignbyte(t[i + 1], t[i], sh);
+}
+
 // The four fp16 pairs "1 + q/16" of the 8 nibbles of v, in the order
 // (byte0 lo, byte2 lo), (byte1 lo, byte3 lo), (byte0 hi, byte2 hi), (byte1 hi, byte3 hi).
 __device__ __forceinline__ void nib_pairs(uint32_t v, uint32_t magic, uint32_t (&p)[4]) {
@@ -167,7 +204,6 @@ struct FQ4K {
         w[4 * i + b] = dsc * (float)((words[i] >> (8 * b + sh)) & 15u) - dm;
   }
 
-  // unit u = (superblock u/4, pair p = u%4): sub-blocks 2p (low nibbles) and 2p+1.
   // unit u = (superblock u/8, quant chunk c = u%8): the 16 bytes qs[16c, 16c+16),
   // i.e. elements l0..l0+15 (l0 = 16*(c%2)) of sub-blocks 2p (low nibbles) and
   // 2p+1 (high nibbles), p = c/2.  Eight consecutive lanes read the eight chunks
@@ -185,6 +221,16 @@ struct FQ4K {
     const uint8_t* blk = row + (u >> 3) * BB;
     return Raw{ld16(blk), ld16(blk + 16 + 16 * (u & 7))};
   }
+  // byte offset of unit u's super-block in the row (w) and in the scale row (s: none)
+  __device__ static uint32_t woff(const QArgs&, int u) { return (uint32_t)(u >> 3) * BB; }
+  __device__ static uint32_t soff(const QArgs&, int) { return 0; }
+  __device__ static Raw load_b(const Src& src, uint32_t wo, uint32_t, int u) {
+    return Raw{bld16(src.w, wo), bld16(src.w, wo + 16 + 16 * (u & 7))};
+  }
+  // Quants enter v_dot2 as fp16 mantissa fields of 1.0: a low nibble (bits 0-3 of a
+  // half) reads 1 + q/1024, a high nibble (bits 4-7) 1 + q/64, so one v_bfi_b32
+  // per pair unpacks them (plus one shift for bytes 1 and 3).  Sub-block A (low
+  // nibbles): sum q x = 1024 (SA - XA); sub-block B (high): 64 (SB - XB).
   __device__ static float dot(const Raw& r, int u, const uint32_t* xa, const float* xg) {
     const int p = (u & 7) >> 1;
     const uint32_t words[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
@@ -193,20 +239,19 @@ struct FQ4K {
     float SA = 0.f, SB = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      uint32_t pr[4];
-      nib_pairs(words[i], magic, pr);
-      SA = dot2(pr[0], xa[2 * i], SA);
-      SA = dot2(pr[1], xa[2 * i + 1], SA);
-      SB = dot2(pr[2], xb[2 * i], SB);
-      SB = dot2(pr[3], xb[2 * i + 1], SB);
+      const uint32_t v = words[i], v8 = v >> 8;
+      SA = dot2(bfi(0x000F000Fu, v, magic), xa[2 * i], SA);        // bytes 0,2 low
+      SA = dot2(bfi(0x000F000Fu, v8, magic), xa[2 * i + 1], SA);   // bytes 1,3 low
+      SB = dot2(bfi(0x00F000F0u, v, magic), xb[2 * i], SB);        // bytes 0,2 high
+      SB = dot2(bfi(0x00F000F0u, v8, magic), xb[2 * i + 1], SB);   // bytes 1,3 high
     }
-    const float d16 = 16.f * h2f(r.h.x), dmin = h2f(r.h.x >> 16);
+    const float d = h2f(r.h.x), dmin = h2f(r.h.x >> 16);
     uint32_t scA, mA, scB, mB;
     Q4kSel(2 * p).get(r.h.y, r.h.z, r.h.w, scA, mA);
     Q4kSel(2 * p + 1).get(r.h.y, r.h.z, r.h.w, scB, mB);
-    const float cA = d16 * (float)scA, cB = d16 * (float)scB;
-    // sum(q x) = 16 (S - X);  w = d sc q - dmin m
-    return cA * SA - (cA + dmin * (float)mA) * xg[0] + cB * SB - (cB + dmin * (float)mB) * xg[1];
+    const float cA = 1024.f * d * (float)scA, cB = 64.f * d * (float)scB;
+    // w = d sc q - dmin m
+    return cA * (SA - xg[0]) + cB * (SB - xg[1]) - dmin * ((float)mA * xg[0] + (float)mB * xg[1]);
   }
 };
 
@@ -238,8 +283,6 @@ struct FQ6K {
       }
   }
 
-  // unit u = (superblock u/4, half h = (u%4)/2, s0 = u%2): elements
-  // 128h+32*s0+l (low nibbles) and 128h+32*(s0+2)+l (high nibbles), l in [0,32).
   // unit u = (superblock u/4, half h = (u%4)/2, s0 = u%2): runs of elements
   // 128h+32*s0+l (low nibbles) and 128h+32*(s0+2)+l (high nibbles), l in [0,32).
   struct Raw { uint32_t ql[8], qh[8], scl, sch, d; };
@@ -256,6 +299,18 @@ struct FQ6K {
     r.scl = ldu16(blk + 192 + 8 * h + 2 * s0);       // scales (s0, l<16), (s0, l>=16)
     r.sch = ldu16(blk + 192 + 8 * h + 2 * s0 + 4);   // scales (s0+2, ...)
     r.d = ldu16(blk + 208);
+    return r;
+  }
+  __device__ static uint32_t woff(const QArgs&, int u) { return (uint32_t)(u >> 2) * BB; }
+  __device__ static uint32_t soff(const QArgs&, int) { return 0; }
+  __device__ static Raw load_b(const Src& src, uint32_t wo, uint32_t, int u) {
+    const int h = (u >> 1) & 1, s0 = u & 1;
+    Raw r;
+    bwords_a2<8>(src.w, wo + 64 * h + 32 * s0, r.ql);
+    bwords_a2<8>(src.w, wo + 128 + 32 * h, r.qh);
+    r.scl = bld2(src.w, wo + 192 + 8 * h + 2 * s0);
+    r.sch = bld2(src.w, wo + 196 + 8 * h + 2 * s0);
+    r.d = bld2(src.w, wo + 208);
     return r;
   }
   __device__ static float dot(const Raw& r, int u, const uint32_t* xlo, const float* xg) {
@@ -325,6 +380,14 @@ struct FQ80 {
     r.d = ldu16(blk);
     return r;
   }
+  __device__ static uint32_t woff(const QArgs&, int u) { return (uint32_t)u * BB; }
+  __device__ static uint32_t soff(const QArgs&, int) { return 0; }
+  __device__ static Raw load_b(const Src& src, uint32_t wo, uint32_t, int) {
+    Raw r;
+    bwords_a2<8>(src.w, wo + 2, r.v);
+    r.d = bld2(src.w, wo);
+    return r;
+  }
   __device__ static float dot(const Raw& r, int, const uint32_t* xp, const float* xg) {
     const float S = q8_words_dot(r.v, xp, 0.f);
     return h2f(r.d) * (256.f * S - 384.f * (xg[0] + xg[1]));   // sum((u-128) x)
@@ -354,6 +417,12 @@ struct FQ80S {
     const uint8_t* q = a.w + n * a.rb + 32 * u;
     const u32x4 q0 = ld16(q), q1 = ld16(q + 16);
     return Raw{{q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w}, a.s[n * (a.K >> 5) + u]};
+  }
+  __device__ static uint32_t woff(const QArgs&, int u) { return 32u * (uint32_t)u; }
+  __device__ static uint32_t soff(const QArgs&, int u) { return 2u * (uint32_t)u; }
+  __device__ static Raw load_b(const Src& src, uint32_t wo, uint32_t so, int) {
+    const u32x4 q0 = bld16(src.w, wo), q1 = bld16(src.w, wo + 16);
+    return Raw{{q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w}, bld2(src.s, so)};
   }
   __device__ static float dot(const Raw& r, int, const uint32_t* xp, const float* xg) {
     const float S = q8_words_dot(r.v, xp, 0.f);
@@ -397,6 +466,17 @@ struct FQ50 {
     ld_words_a2<4>(blk + 6, r.qs);
     r.qh = qh1[0];
     r.d = ldu16(blk);
+    return r;
+  }
+  __device__ static uint32_t woff(const QArgs&, int u) { return (uint32_t)u * BB; }
+  __device__ static uint32_t soff(const QArgs&, int) { return 0; }
+  __device__ static Raw load_b(const Src& src, uint32_t wo, uint32_t, int) {
+    Raw r;
+    uint32_t qh1[1];
+    bwords_a2<1>(src.w, wo + 2, qh1);
+    bwords_a2<4>(src.w, wo + 6, r.qs);
+    r.qh = qh1[0];
+    r.d = bld2(src.w, wo);
     return r;
   }
   __device__ static float dot(const Raw& r, int, const uint32_t* xp, const float* xg) {
@@ -448,6 +528,11 @@ struct FQ50S {
     const int64_t off = n * a.rb + 16 * u;
     return Raw{ld16(a.w + off), ld16(a.aux + off), a.s[n * (a.K >> 5) + u]};
   }
+  __device__ static uint32_t woff(const QArgs&, int u) { return 16u * (uint32_t)u; }
+  __device__ static uint32_t soff(const QArgs&, int u) { return 2u * (uint32_t)u; }
+  __device__ static Raw load_b(const Src& src, uint32_t wo, uint32_t so, int) {
+    return Raw{bld16(src.w, wo), bld16(src.aux, wo), bld2(src.s, so)};
+  }
   __device__ static float dot(const Raw& r, int, const uint32_t* xp, const float* xg) {
     const uint32_t qv[4] = {r.q.x, r.q.y, r.q.z, r.q.w}, hv[4] = {r.hq.x, r.hq.y, r.hq.z, r.hq.w};
     const uint32_t magic = MAGIC1;
@@ -489,6 +574,11 @@ struct FMLX {
   __device__ static Raw load(const QArgs& a, int64_t n, int u) {
     const int64_t gi = n * (a.K / a.gs) + (32 * u) / a.gs;
     return Raw{ld16(a.w + n * a.rb + 16 * u), a.s[gi], a.b[gi]};
+  }
+  __device__ static uint32_t woff(const QArgs&, int u) { return 16u * (uint32_t)u; }
+  __device__ static uint32_t soff(const QArgs& a, int u) { return 2u * (uint32_t)((32 * u) / a.gs); }
+  __device__ static Raw load_b(const Src& src, uint32_t wo, uint32_t so, int) {
+    return Raw{bld16(src.w, wo), bld2(src.s, so), bld2(src.b, so)};
   }
   __device__ static float dot(const Raw& r, int, const uint32_t* xp, const float* xg) {
     const uint32_t v[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
