@@ -1,6 +1,8 @@
 // Dense quantized matmul kernels for gfx950: dequant probe, M=1 GEMV (v_dot2),
 // M<=16 GEMV on MFMA, and the prefill GEMM on MFMA.  All launched on the caller's
 // HIP stream; no allocation, no global mutable state.
+#include <type_traits>
+
 #include "launch.h"
 
 namespace alloy {
@@ -522,6 +524,157 @@ __global__ __launch_bounds__(256) void k_gemm(QArgs a, const XT* x, int M, void*
 }
 
 // ------------------------------------------------------------------ host launchers
+// ------------------------------------------------------------------ prefill GEMM, Q4_K, 256x256
+// 512 threads = 8 waves as 2 (x rows) x 4 (weight rows); each wave owns a 128x64 output
+// block = 4 x 2 tiles of v_mfma_f32_32x32x16_f16 (128 fp32 accumulators).  K advances
+// in steps of 64 through double-buffered LDS (x tile and dequantised weight tile, rows
+// padded to 72 halves: 144 KB): the next step's global loads are issued before the
+// current step's MFMAs, its weight tile is dequantised and both tiles are written to
+// the other buffer after them, one barrier per step.  All global traffic uses buffer
+// resources, so rows past M or N read as zero and stores past them are dropped; the
+// loads of the step after the last one are harmless and never consumed.
+//
+// Weight dequant, two threads per weight row (one Q4_K sub-block of 32 each): the
+// nibbles are masked into the two halves of a dword as fp16 denormals q*2^-24 (or
+// 16q*2^-24 for high nibbles), and v_fma_mix{lo,hi}_f16 computes
+// RN16((d*sc*2^24[/16]) * that - dmin*m) in one fused step: the exact fp32 weight
+// rounded once to fp16.
+constexpr int QBM = 256, QBN = 256, QBK = 64, QLD = 72;
+
+__device__ __forceinline__ uint32_t mix_lo(uint32_t d, uint32_t q, float s, float c) {   // q.lo
+  asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "+v"(d) : "v"(q), "v"(s), "v"(c));
+  return d;
+}
+__device__ __forceinline__ uint32_t mix_hi(uint32_t d, uint32_t q, float s, float c) {   // q.lo
+  asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "+v"(d) : "v"(q), "v"(s), "v"(c));
+  return d;
+}
+__device__ __forceinline__ uint32_t mix_lo_h(uint32_t d, uint32_t q, float s, float c) { // q.hi
+  asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(d) : "v"(q), "v"(s), "v"(c));
+  return d;
+}
+__device__ __forceinline__ uint32_t mix_hi_h(uint32_t d, uint32_t q, float s, float c) { // q.hi
+  asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(d) : "v"(q), "v"(s), "v"(c));
+  return d;
+}
+
+template <typename YT>
+__global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, YT* y, int N) {
+  __shared__ __attribute__((aligned(16))) f16 As[2][QBM][QLD];
+  __shared__ __attribute__((aligned(16))) f16 Bs[2][QBN][QLD];
+  const int K = a.K, KT = K / QBK;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int m0 = (int)blockIdx.y * QBM, n0 = (int)blockIdx.x * QBN;
+  const uint32_t rb = (uint32_t)a.rb;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)x, (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), ALLOY_RSRC_DW3);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.w, (short)0, (int)((uint32_t)N * rb), ALLOY_RSRC_DW3);
+  // x tile: 256 rows x 8 chunks of 16 B, four chunks per thread (8 lanes per row)
+  uint32_t xoff[4];
+  int arow[4], acol[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + 512 * i;
+    arow[i] = c >> 3;
+    acol[i] = (c & 7) * 8;
+    xoff[i] = ((uint32_t)(m0 + arow[i]) * (uint32_t)K + (uint32_t)acol[i]) * 2u;
+  }
+  // weight tile: row br, sub-block half bh (elements 32bh .. 32bh+31 of the step)
+  const int br = tid >> 1, bh = tid & 1;
+  const uint32_t wrow = (uint32_t)(n0 + br) * rb;
+  const uint32_t qmask = bh ? 0x00F000F0u : 0x000F000Fu;
+  const float qscale = bh ? 1048576.f : 16777216.f;      // 2^24 / (16 for high nibbles)
+
+  u32x4 xs[4], hd, q0, q1;
+  auto gload = [&](int kt) {
+    const uint32_t k0 = (uint32_t)kt * QBK;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xs[i] = bld16(xr, xoff[i] + 2u * k0);
+    const uint32_t blk = wrow + (k0 >> 8) * 144u;
+    hd = bld16(wr, blk);
+    const uint32_t qo = blk + 16u + 32u * ((k0 >> 6) & 3u);
+    q0 = bld16(wr, qo);
+    q1 = bld16(wr, qo + 16u);
+  };
+  auto lstore = [&](int kt, int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *(u32x4*)&As[buf][arow[i]][acol[i]] = xs[i];
+    // sub-block g = 2p + bh of super-block k0/256
+    const int g = 2 * ((kt & 3)) + bh;
+    uint32_t sc, mn;
+    Q4kSel(g).get(hd.y, hd.z, hd.w, sc, mn);       // branch-free: g differs across lanes
+    const float s = h2f(hd.x) * (float)sc * qscale;
+    const float c = -(h2f(hd.x >> 16) * (float)mn);
+    const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    uint32_t o[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t ea = w[i] & qmask, eb = (w[i] >> 8) & qmask;   // (e0, e2), (e1, e3)
+      o[2 * i] = mix_hi(mix_lo(0u, ea, s, c), eb, s, c);
+      o[2 * i + 1] = mix_hi_h(mix_lo_h(0u, ea, s, c), eb, s, c);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *(u32x4*)&Bs[buf][br][32 * bh + 8 * j] = u32x4{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
+  };
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  gload(0);
+  lstore(0, 0);
+  __syncthreads();
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    gload(kt + 1);                      // past the end: in-bounds garbage or zeros, unused
+#pragma unroll
+    for (int ks = 0; ks < QBK; ks += 16) {
+      const int kc = ks + 8 * (lane >> 5);
+      f16x8 af[4], bf[2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) af[i] = *(const f16x8*)&As[cur][128 * wm + 32 * i + (lane & 31)][kc];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bf[j] = *(const f16x8*)&Bs[cur][64 * wn + 32 * j + (lane & 31)][kc];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    lstore(kt + 1, cur ^ 1);
+    __syncthreads();
+  }
+  // D[i][j] of a tile: j = lane%32 (weight row), i = 8(t/4) + 4(lane/32) + t%4 (x row)
+  constexpr uint32_t esz = sizeof(YT);
+  const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)y, (short)0, (int)((uint32_t)M * (uint32_t)N * esz), ALLOY_RSRC_DW3);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + 64 * wn + 32 * j + (lane & 31);
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const int m = m0 + 128 * wm + 32 * i + 8 * (t >> 2) + 4 * (lane >> 5) + (t & 3);
+        const uint32_t off = n < N ? ((uint32_t)m * (uint32_t)N + (uint32_t)n) * esz : 0x80000000u;
+        // copy the element out first: a bit_cast applied to the vector element
+        // directly picked element 0 for every t in this compiler
+        const float v = acc[i][j][t];
+        if constexpr (sizeof(YT) == 4)
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), yr, off, 0, 0);
+        else
+          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (f16)v), yr, off, 0, 0);
+      }
+    }
+}
+
 template <template <class> class Fn, typename... Args>
 static hipError_t by_fmt(int fmt, Args&&... args) {
   switch (fmt) {
@@ -740,7 +893,20 @@ hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, 
 template <class F>
 struct GemmRun {
   static hipError_t run(const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32, int64_t M,
-                        int64_t N, const Opts&, hipStream_t st) {
+                        int64_t N, const Opts& o, hipStream_t st) {
+    if constexpr (std::is_same<F, FQ4K>::value) {
+      // 256x256 tiles once there are x rows enough to fill them; 32-bit buffer offsets
+      const bool fits = (uint64_t)M * (uint64_t)a.K * 2u < (1ull << 31) && (uint64_t)N * (uint64_t)a.rb < (1ull << 31) &&
+                        (uint64_t)M * (uint64_t)N * 4u < (1ull << 31);
+      if (!x_f32 && fits && (M > 128 || o.variant == 4) && o.variant != 1) {
+        const dim3 grid((unsigned)((N + QBN - 1) / QBN), (unsigned)((M + QBM - 1) / QBM));
+        if (y_f32)
+          hipLaunchKernelGGL((k_gemm_q4k<float>), grid, dim3(512), 0, st, a, (const f16*)x, (int)M, (float*)y, (int)N);
+        else
+          hipLaunchKernelGGL((k_gemm_q4k<f16>), grid, dim3(512), 0, st, a, (const f16*)x, (int)M, (f16*)y, (int)N);
+        return hipGetLastError();
+      }
+    }
     dim3 grid((unsigned)((N + GBN - 1) / GBN), (unsigned)((M + GBM - 1) / GBM));
     if (x_f32)
       hipLaunchKernelGGL((k_gemm<F, float>), grid, dim3(256), 0, st, a, (const float*)x, (int)M, y, (int)y_f32, N);
