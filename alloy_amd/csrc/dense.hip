@@ -539,18 +539,21 @@ __global__ __launch_bounds__(256) void k_gemm(QArgs a, const XT* x, int M, void*
 // 16q*2^-24 for high nibbles), and v_fma_mix{lo,hi}_f16 computes
 // RN16((d*sc*2^24[/16]) * that - dmin*m) in one fused step: the exact fp32 weight
 // rounded once to fp16.
-constexpr int QBM = 256, QBN = 256, QBK = 64, QLD = 72;
+constexpr int QBK = 64, QLD = 72;
 
-__device__ __forceinline__ uint32_t mix_lo(uint32_t d, uint32_t q, float s, float c) {   // q.lo
-  asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "+v"(d) : "v"(q), "v"(s), "v"(c));
+// mix_lo* start a dword (the high half is left undefined for a following mix_hi*)
+__device__ __forceinline__ uint32_t mix_lo(uint32_t q, float s, float c) {               // q.lo
+  uint32_t d;
+  asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(q), "v"(s), "v"(c));
   return d;
 }
 __device__ __forceinline__ uint32_t mix_hi(uint32_t d, uint32_t q, float s, float c) {   // q.lo
   asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "+v"(d) : "v"(q), "v"(s), "v"(c));
   return d;
 }
-__device__ __forceinline__ uint32_t mix_lo_h(uint32_t d, uint32_t q, float s, float c) { // q.hi
-  asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(d) : "v"(q), "v"(s), "v"(c));
+__device__ __forceinline__ uint32_t mix_lo_h(uint32_t q, float s, float c) {             // q.hi
+  uint32_t d;
+  asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(q), "v"(s), "v"(c));
   return d;
 }
 __device__ __forceinline__ uint32_t mix_hi_h(uint32_t d, uint32_t q, float s, float c) { // q.hi
@@ -558,8 +561,11 @@ __device__ __forceinline__ uint32_t mix_hi_h(uint32_t d, uint32_t q, float s, fl
   return d;
 }
 
-template <typename YT>
+// MI x NI: 32x32 MFMA tiles per wave; the 8 waves sit as 2 (x rows) x 4 (weight rows),
+// so a workgroup tile is QBM = 64*MI x QBN = 128*NI.
+template <int MI, int NI, typename YT>
 __global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, YT* y, int N) {
+  constexpr int QBM = 64 * MI, QBN = 128 * NI, AC = QBM / 64;   // AC: x chunks per thread
   __shared__ __attribute__((aligned(16))) f16 As[2][QBM][QLD];
   __shared__ __attribute__((aligned(16))) f16 Bs[2][QBN][QLD];
   const int K = a.K, KT = K / QBK;
@@ -571,98 +577,127 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, 
       (void*)x, (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), ALLOY_RSRC_DW3);
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)a.w, (short)0, (int)((uint32_t)N * rb), ALLOY_RSRC_DW3);
-  // x tile: 256 rows x 8 chunks of 16 B, four chunks per thread (8 lanes per row)
-  uint32_t xoff[4];
-  int arow[4], acol[4];
+  // x tile: QBM rows x 8 chunks of 16 B, AC chunks per thread (8 lanes per row)
+  uint32_t xoff[AC];
+  int arow[AC], acol[AC];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < AC; ++i) {
     const int c = tid + 512 * i;
     arow[i] = c >> 3;
     acol[i] = (c & 7) * 8;
     xoff[i] = ((uint32_t)(m0 + arow[i]) * (uint32_t)K + (uint32_t)acol[i]) * 2u;
   }
-  // weight tile: row br, sub-block half bh (elements 32bh .. 32bh+31 of the step)
-  const int br = tid >> 1, bh = tid & 1;
+  // weight tile: row br, sub-block half bh (elements 32bh .. 32bh+31 of the step);
+  // with QBN = 128 the upper half of the threads mirror the lower half's rows (their
+  // stores land on the same LDS bytes with the same values)
+  const int br = (tid >> 1) & (QBN - 1), bh = tid & 1;
   const uint32_t wrow = (uint32_t)(n0 + br) * rb;
   const uint32_t qmask = bh ? 0x00F000F0u : 0x000F000Fu;
   const float qscale = bh ? 1048576.f : 16777216.f;      // 2^24 / (16 for high nibbles)
 
-  u32x4 xs[4], hd, q0, q1;
-  auto gload = [&](int kt) {
+  // raw bytes of a step: x chunks, Q4_K header, 32 quant bytes
+  struct Raw { u32x4 xs[AC], hd, q0, q1; };
+  auto gload = [&](int kt, Raw& r) {
     const uint32_t k0 = (uint32_t)kt * QBK;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xs[i] = bld16(xr, xoff[i] + 2u * k0);
+    for (int i = 0; i < AC; ++i) r.xs[i] = bld16(xr, xoff[i] + 2u * k0);
     const uint32_t blk = wrow + (k0 >> 8) * 144u;
-    hd = bld16(wr, blk);
+    r.hd = bld16(wr, blk);
     const uint32_t qo = blk + 16u + 32u * ((k0 >> 6) & 3u);
-    q0 = bld16(wr, qo);
-    q1 = bld16(wr, qo + 16u);
+    r.q0 = bld16(wr, qo);
+    r.q1 = bld16(wr, qo + 16u);
   };
-  auto lstore = [&](int kt, int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *(u32x4*)&As[buf][arow[i]][acol[i]] = xs[i];
-    // sub-block g = 2p + bh of super-block k0/256
-    const int g = 2 * ((kt & 3)) + bh;
+  // scale/offset of this thread's sub-block g = 2p + bh of the step's super-block
+  auto scales = [&](int kt, const Raw& r, float& s, float& c) {
     uint32_t sc, mn;
-    Q4kSel(g).get(hd.y, hd.z, hd.w, sc, mn);       // branch-free: g differs across lanes
-    const float s = h2f(hd.x) * (float)sc * qscale;
-    const float c = -(h2f(hd.x >> 16) * (float)mn);
-    const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    uint32_t o[16];
+    Q4kSel(2 * (kt & 3) + bh).get(r.hd.y, r.hd.z, r.hd.w, sc, mn);   // branch-free
+    s = h2f(r.hd.x) * (float)sc * qscale;
+    c = -(h2f(r.hd.x >> 16) * (float)mn);
+  };
+  // quarter j of the dequant: words 2j, 2j+1 -> 8 halves -> Bs[buf][br][32bh + 8j]
+  auto deq = [&](const Raw& r, int j, float s, float c, int buf) {
+    const uint32_t w0 = j < 2 ? (j == 0 ? r.q0.x : r.q0.z) : (j == 2 ? r.q1.x : r.q1.z);
+    const uint32_t w1 = j < 2 ? (j == 0 ? r.q0.y : r.q0.w) : (j == 2 ? r.q1.y : r.q1.w);
+    uint32_t o[4];
+    const uint32_t ws[2] = {w0, w1};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t ea = w[i] & qmask, eb = (w[i] >> 8) & qmask;   // (e0, e2), (e1, e3)
-      o[2 * i] = mix_hi(mix_lo(0u, ea, s, c), eb, s, c);
-      o[2 * i + 1] = mix_hi_h(mix_lo_h(0u, ea, s, c), eb, s, c);
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t ea = ws[i] & qmask, eb = (ws[i] >> 8) & qmask;   // (e0, e2), (e1, e3)
+      o[2 * i] = mix_hi(mix_lo(ea, s, c), eb, s, c);
+      o[2 * i + 1] = mix_hi_h(mix_lo_h(ea, s, c), eb, s, c);
     }
+    *(u32x4*)&Bs[buf][br][32 * bh + 8 * j] = u32x4{o[0], o[1], o[2], o[3]};
+  };
+  auto astore = [&](const Raw& r, int buf) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      *(u32x4*)&Bs[buf][br][32 * bh + 8 * j] = u32x4{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
+    for (int i = 0; i < AC; ++i) *(u32x4*)&As[buf][arow[i]][acol[i]] = r.xs[i];
   };
 
-  f32x16 acc[4][2];
+  f32x16 acc[MI][NI];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NI; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  gload(0);
-  lstore(0, 0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    gload(kt + 1);                      // past the end: in-bounds garbage or zeros, unused
+  // raw data runs three steps ahead of the MFMAs, LDS one step ahead: while step kt
+  // multiplies from buffer kt%2, step kt+1 (loaded during step kt-2) is dequantised
+  // into the other buffer in quarters between the MFMA groups, and step kt+3 loads
+  Raw ra, rb2;
+  gload(0, ra);
+  gload(1, rb2);
+  {
+    float s, c;
+    scales(0, ra, s, c);
 #pragma unroll
-    for (int ks = 0; ks < QBK; ks += 16) {
-      const int kc = ks + 8 * (lane >> 5);
-      f16x8 af[4], bf[2];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) af[i] = *(const f16x8*)&As[cur][128 * wm + 32 * i + (lane & 31)][kc];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) bf[j] = *(const f16x8*)&Bs[cur][64 * wn + 32 * j + (lane & 31)][kc];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-    lstore(kt + 1, cur ^ 1);
-    __syncthreads();
+    for (int j = 0; j < 4; ++j) deq(ra, j, s, c, 0);
+    astore(ra, 0);
   }
+  gload(2, ra);
+  __syncthreads();
+  // nxt holds step kt+1 on entry and is reloaded with step kt+3
+  auto step = [&](int kt, Raw& nxt) {
+    const int cur = kt & 1;
+    float s, c;
+    scales(kt + 1, nxt, s, c);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int kc = 16 * ks + 8 * (lane >> 5);
+      f16x8 af[MI], bf[NI];
+#pragma unroll
+      for (int i = 0; i < MI; ++i) af[i] = *(const f16x8*)&As[cur][32 * MI * wm + 32 * i + (lane & 31)][kc];
+#pragma unroll
+      for (int j = 0; j < NI; ++j) bf[j] = *(const f16x8*)&Bs[cur][32 * NI * wn + 32 * j + (lane & 31)][kc];
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+      deq(nxt, ks, s, c, cur ^ 1);
+    }
+    astore(nxt, cur ^ 1);
+    gload(kt + 3, nxt);                 // past the end: in-bounds garbage or zeros, unused
+    __syncthreads();
+  };
+  int kt = 0;
+  for (; kt + 1 < KT; kt += 2) {
+    step(kt, rb2);
+    step(kt + 1, ra);
+  }
+  if (kt < KT) step(kt, rb2);
   // D[i][j] of a tile: j = lane%32 (weight row), i = 8(t/4) + 4(lane/32) + t%4 (x row)
   constexpr uint32_t esz = sizeof(YT);
   const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)y, (short)0, (int)((uint32_t)M * (uint32_t)N * esz), ALLOY_RSRC_DW3);
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = n0 + 64 * wn + 32 * j + (lane & 31);
+    for (int j = 0; j < NI; ++j) {
+      const int n = n0 + 32 * NI * wn + 32 * j + (lane & 31);
 #pragma unroll
       for (int t = 0; t < 16; ++t) {
-        const int m = m0 + 128 * wm + 32 * i + 8 * (t >> 2) + 4 * (lane >> 5) + (t & 3);
+        const int m = m0 + 32 * MI * wm + 32 * i + 8 * (t >> 2) + 4 * (lane >> 5) + (t & 3);
         const uint32_t off = n < N ? ((uint32_t)m * (uint32_t)N + (uint32_t)n) * esz : 0x80000000u;
         // copy the element out first: a bit_cast applied to the vector element
         // directly picked element 0 for every t in this compiler
@@ -898,13 +933,22 @@ struct GemmRun {
       // 256x256 tiles once there are x rows enough to fill them; 32-bit buffer offsets
       const bool fits = (uint64_t)M * (uint64_t)a.K * 2u < (1ull << 31) && (uint64_t)N * (uint64_t)a.rb < (1ull << 31) &&
                         (uint64_t)M * (uint64_t)N * 4u < (1ull << 31);
-      if (!x_f32 && fits && (M > 128 || o.variant == 4) && o.variant != 1) {
-        const dim3 grid((unsigned)((N + QBN - 1) / QBN), (unsigned)((M + QBM - 1) / QBM));
-        if (y_f32)
-          hipLaunchKernelGGL((k_gemm_q4k<float>), grid, dim3(512), 0, st, a, (const f16*)x, (int)M, (float*)y, (int)N);
-        else
-          hipLaunchKernelGGL((k_gemm_q4k<f16>), grid, dim3(512), 0, st, a, (const f16*)x, (int)M, (f16*)y, (int)N);
-        return hipGetLastError();
+      if (!x_f32 && fits && (M > 64 || o.variant >= 4) && o.variant != 1) {
+        // largest tile that still gives every CU a workgroup (256 CUs), else the smallest
+        auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+        int kind = o.variant >= 4 ? o.variant - 4 : (tiles(256, 256) >= 256 ? 0 : tiles(128, 256) >= 256 ? 1 : 2);
+        auto go = [&](auto mi, auto ni) {
+          constexpr int MI = decltype(mi)::value, NI = decltype(ni)::value;
+          const dim3 grid((unsigned)((N + 128 * NI - 1) / (128 * NI)), (unsigned)((M + 64 * MI - 1) / (64 * MI)));
+          if (y_f32)
+            hipLaunchKernelGGL((k_gemm_q4k<MI, NI, float>), grid, dim3(512), 0, st, a, (const f16*)x, (int)M, (float*)y, (int)N);
+          else
+            hipLaunchKernelGGL((k_gemm_q4k<MI, NI, f16>), grid, dim3(512), 0, st, a, (const f16*)x, (int)M, (f16*)y, (int)N);
+          return hipGetLastError();
+        };
+        if (kind == 0) return go(std::integral_constant<int, 4>(), std::integral_constant<int, 2>());
+        if (kind == 1) return go(std::integral_constant<int, 2>(), std::integral_constant<int, 2>());
+        return go(std::integral_constant<int, 2>(), std::integral_constant<int, 1>());
       }
     }
     dim3 grid((unsigned)((N + GBN - 1) / GBN), (unsigned)((M + GBM - 1) / GBM));

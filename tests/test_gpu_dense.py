@@ -129,8 +129,14 @@ def test_gemm(dev, fmt, M, N, K):
     rng = np.random.default_rng(M * N)
     wt = Weight(fmt, N, K, rng, dev)
     x = synth.numpy_x(M, K, rng)
-    y = wt.qmm(torch.from_numpy(x).to(dev), path="gemm", out_dtype=torch.float32).cpu().numpy()
+    xt = torch.from_numpy(x).to(dev)
+    y = wt.qmm(xt, path="gemm", out_dtype=torch.float32).cpu().numpy()
     check(y, x, wt.W, f"{fmt} gemm M={M} N={N} K={K}")
+    if fmt == "q4_k":
+        # every kernel: 1 = 128x128 generic, 4/5/6 = Q4_K 256x256 / 128x256 / 128x128 tiles
+        for variant in (1, 4, 5, 6):
+            yv = wt.qmm(xt, path="gemm", out_dtype=torch.float32, opts=variant << 36).cpu().numpy()
+            check(yv, x, wt.W, f"{fmt} gemm M={M} N={N} K={K} variant={variant}")
 
 
 def test_outputs_deterministic_and_f16(dev):
