@@ -534,9 +534,9 @@ __global__ __launch_bounds__(256) void k_gemm(QArgs a, const XT* x, int M, void*
 // resources, so rows past M or N read as zero and stores past them are dropped; the
 // loads of the step after the last one are harmless and never consumed.
 //
-// Weight dequant, two threads per weight row (one Q4_K sub-block of 32 each): the
-// nibbles are masked into the two halves of a dword as fp16 denormals q*2^-24 (or
-// 16q*2^-24 for high nibbles), and v_fma_mix{lo,hi}_f16 computes
+// Weight dequant, two threads per weight row (16 of the step's 32 quant bytes each):
+// the nibbles are masked into the two halves of a dword as fp16 denormals q*2^-24
+// (or 16q*2^-24 for high nibbles), and v_fma_mix{lo,hi}_f16 computes
 // RN16((d*sc*2^24[/16]) * that - dmin*m) in one fused step: the exact fp32 weight
 // rounded once to fp16.
 constexpr int QBK = 64, QLD = 72;
@@ -587,50 +587,58 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, 
     acol[i] = (c & 7) * 8;
     xoff[i] = ((uint32_t)(m0 + arow[i]) * (uint32_t)K + (uint32_t)acol[i]) * 2u;
   }
-  // weight tile: row br, sub-block half bh (elements 32bh .. 32bh+31 of the step);
-  // with QBN = 128 the upper half of the threads mirror the lower half's rows (their
-  // stores land on the same LDS bytes with the same values)
+  // weight tile: row br; thread half bh owns quant bytes 32p + 16bh .. +15 of every
+  // pair p, i.e. elements 16bh + [0,16) (low nibbles, sub-block 2p) and
+  // 32 + 16bh + [0,16) (high nibbles, sub-block 2p+1) of step p of a super-block.
+  // A thread loads its 80 bytes of a super-block (header + 4 x 16 quant bytes) in one
+  // burst every four steps, so each weight line is fetched into L1 once.  With
+  // QBN = 128 the upper half of the threads mirror the lower half's rows.
   const int br = (tid >> 1) & (QBN - 1), bh = tid & 1;
   const uint32_t wrow = (uint32_t)(n0 + br) * rb;
-  const uint32_t qmask = bh ? 0x00F000F0u : 0x000F000Fu;
-  const float qscale = bh ? 1048576.f : 16777216.f;      // 2^24 / (16 for high nibbles)
 
-  // raw bytes of a step: x chunks, Q4_K header, 32 quant bytes
-  struct Raw { u32x4 xs[AC], hd, q0, q1; };
-  auto gload = [&](int kt, Raw& r) {
-    const uint32_t k0 = (uint32_t)kt * QBK;
-#pragma unroll
-    for (int i = 0; i < AC; ++i) r.xs[i] = bld16(xr, xoff[i] + 2u * k0);
-    const uint32_t blk = wrow + (k0 >> 8) * 144u;
+  struct Blk { u32x4 hd, q[4]; };          // this thread's bytes of one super-block
+  auto bload = [&](int sb, Blk& r) {       // past the end: in-bounds garbage or zeros
+    const uint32_t blk = wrow + (uint32_t)sb * 144u;
     r.hd = bld16(wr, blk);
-    const uint32_t qo = blk + 16u + 32u * ((k0 >> 6) & 3u);
-    r.q0 = bld16(wr, qo);
-    r.q1 = bld16(wr, qo + 16u);
-  };
-  // scale/offset of this thread's sub-block g = 2p + bh of the step's super-block
-  auto scales = [&](int kt, const Raw& r, float& s, float& c) {
-    uint32_t sc, mn;
-    Q4kSel(2 * (kt & 3) + bh).get(r.hd.y, r.hd.z, r.hd.w, sc, mn);   // branch-free
-    s = h2f(r.hd.x) * (float)sc * qscale;
-    c = -(h2f(r.hd.x >> 16) * (float)mn);
-  };
-  // quarter j of the dequant: words 2j, 2j+1 -> 8 halves -> Bs[buf][br][32bh + 8j]
-  auto deq = [&](const Raw& r, int j, float s, float c, int buf) {
-    const uint32_t w0 = j < 2 ? (j == 0 ? r.q0.x : r.q0.z) : (j == 2 ? r.q1.x : r.q1.z);
-    const uint32_t w1 = j < 2 ? (j == 0 ? r.q0.y : r.q0.w) : (j == 2 ? r.q1.y : r.q1.w);
-    uint32_t o[4];
-    const uint32_t ws[2] = {w0, w1};
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t ea = ws[i] & qmask, eb = (ws[i] >> 8) & qmask;   // (e0, e2), (e1, e3)
-      o[2 * i] = mix_hi(mix_lo(ea, s, c), eb, s, c);
-      o[2 * i + 1] = mix_hi_h(mix_lo_h(ea, s, c), eb, s, c);
+    for (int p = 0; p < 4; ++p) r.q[p] = bld16(wr, blk + 16u + 32u * p + 16u * (uint32_t)bh);
+  };
+  u32x4 xs[AC];                            // x chunks of the next step
+  auto xload = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < AC; ++i) xs[i] = bld16(xr, xoff[i] + 2u * (uint32_t)kt * QBK);
+  };
+  auto astore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < AC; ++i) *(u32x4*)&As[buf][arow[i]][acol[i]] = xs[i];
+  };
+  // scales/offsets of sub-blocks 2p (low nibbles) and 2p+1 (high) of pair p; the
+  // nibble halves enter v_fma_mix as fp16 denormals q*2^-24 (16q*2^-24 high)
+  auto scales = [&](const Blk& r, int p, float (&s)[2], float (&c)[2]) {
+    uint32_t sc0, mn0, sc1, mn1;
+    q4k_scale_min(r.hd.y, r.hd.z, r.hd.w, 2 * p, sc0, mn0);     // p is a constant
+    q4k_scale_min(r.hd.y, r.hd.z, r.hd.w, 2 * p + 1, sc1, mn1);
+    const float d = h2f(r.hd.x), dmin = h2f(r.hd.x >> 16);
+    s[0] = d * (float)sc0 * 16777216.f;                 // 2^24
+    s[1] = d * (float)sc1 * 1048576.f;                  // 2^24 / 16
+    c[0] = -(dmin * (float)mn0);
+    c[1] = -(dmin * (float)mn1);
+  };
+  // quarter j of a step's dequant: word j of the pair -> 4 elements of each sub-block
+  auto deq = [&](const u32x4& q, int j, const float (&s)[2], const float (&c)[2], int buf) {
+    const uint32_t w = j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
+    const uint32_t w8 = w >> 8;
+    uint32_t o[2][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t m = h ? 0x00F000F0u : 0x000F000Fu;
+      const uint32_t ea = w & m, eb = w8 & m;                 // (e0, e2), (e1, e3)
+      o[h][0] = mix_hi(mix_lo(ea, s[h], c[h]), eb, s[h], c[h]);
+      o[h][1] = mix_hi_h(mix_lo_h(ea, s[h], c[h]), eb, s[h], c[h]);
     }
-    *(u32x4*)&Bs[buf][br][32 * bh + 8 * j] = u32x4{o[0], o[1], o[2], o[3]};
-  };
-  auto astore = [&](const Raw& r, int buf) {
-#pragma unroll
-    for (int i = 0; i < AC; ++i) *(u32x4*)&As[buf][arow[i]][acol[i]] = r.xs[i];
+    // elements 16bh + 4j + [0,4) and 32 + 16bh + 4j + [0,4)
+    *(uint2*)&Bs[buf][br][16 * bh + 4 * j] = uint2{o[0][0], o[0][1]};
+    *(uint2*)&Bs[buf][br][32 + 16 * bh + 4 * j] = uint2{o[1][0], o[1][1]};
   };
 
   f32x16 acc[MI][NI];
@@ -641,26 +649,19 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, 
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  // raw data runs three steps ahead of the MFMAs, LDS one step ahead: while step kt
-  // multiplies from buffer kt%2, step kt+1 (loaded during step kt-2) is dequantised
-  // into the other buffer in quarters between the MFMA groups, and step kt+3 loads
-  Raw ra, rb2;
-  gload(0, ra);
-  gload(1, rb2);
-  {
-    float s, c;
-    scales(0, ra, s, c);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) deq(ra, j, s, c, 0);
-    astore(ra, 0);
-  }
-  gload(2, ra);
-  __syncthreads();
-  // nxt holds step kt+1 on entry and is reloaded with step kt+3
-  auto step = [&](int kt, Raw& nxt) {
+  // Step kt multiplies from LDS buffer kt%2 while step kt+1 is dequantised into the
+  // other buffer in quarters between its MFMA groups and the x chunks of step kt+1
+  // (loaded during step kt-1) are stored; super-block raw bytes are loaded four
+  // steps before their first use.  nb: the super-block holding step kt+1's pair.
+  auto step = [&](int kt, const Blk& nb, int np) {
     const int cur = kt & 1;
-    float s, c;
-    scales(kt + 1, nxt, s, c);
+    float s[2], c[2];
+    scales(nb, np, s, c);
+    const u32x4 q = nb.q[np];
+    u32x4 xk[AC];
+#pragma unroll
+    for (int i = 0; i < AC; ++i) xk[i] = xs[i];
+    xload(kt + 2);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int kc = 16 * ks + 8 * (lane >> 5);
@@ -674,18 +675,50 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, 
 #pragma unroll
         for (int j = 0; j < NI; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-      deq(nxt, ks, s, c, cur ^ 1);
+      deq(q, ks, s, c, cur ^ 1);
     }
-    astore(nxt, cur ^ 1);
-    gload(kt + 3, nxt);                 // past the end: in-bounds garbage or zeros, unused
+#pragma unroll
+    for (int i = 0; i < AC; ++i) *(u32x4*)&As[cur ^ 1][arow[i]][acol[i]] = xk[i];
     __syncthreads();
   };
-  int kt = 0;
-  for (; kt + 1 < KT; kt += 2) {
-    step(kt, rb2);
-    step(kt + 1, ra);
+
+  Blk b0, b1;
+  bload(0, b0);
+  bload(1, b1);
+  xload(0);
+  {
+    float s[2], c[2];
+    scales(b0, 0, s, c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) deq(b0.q[0], j, s, c, 0);
+    astore(0);
   }
-  if (kt < KT) step(kt, rb2);
+  xload(1);
+  __syncthreads();
+  // super-blocks in pairs: steps 4S..4S+3 use b0 (pairs 1..3 of S) then b1 (pair 0
+  // of S+1); b0 is reloaded with S+2 once its last pair has been dequantised
+  const int SB = KT / 4;
+  int S = 0;
+  for (; S + 1 < SB; S += 2) {
+    const int kt = 4 * S;
+    step(kt, b0, 1);
+    step(kt + 1, b0, 2);
+    step(kt + 2, b0, 3);
+    bload(S + 2, b0);
+    step(kt + 3, b1, 0);
+    step(kt + 4, b1, 1);
+    step(kt + 5, b1, 2);
+    step(kt + 6, b1, 3);
+    bload(S + 3, b1);
+    step(kt + 7, b0, 0);
+  }
+  if (S < SB) {                            // last super-block (odd count)
+    const int kt = 4 * S;
+    step(kt, b0, 1);
+    step(kt + 1, b0, 2);
+    step(kt + 2, b0, 3);
+    step(kt + 3, b1, 0);                   // dequantises garbage into an unused buffer
+  }
   // D[i][j] of a tile: j = lane%32 (weight row), i = 8(t/4) + 4(lane/32) + t%4 (x row)
   constexpr uint32_t esz = sizeof(YT);
   const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
