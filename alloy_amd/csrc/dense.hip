@@ -676,6 +676,12 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, 
         for (int j = 0; j < NI; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
       deq(q, ks, s, c, cur ^ 1);
+      // keep the last MFMAs' operands live across the dequant: its v_fma_mix results
+      // come from inline asm, which the hazard recognizer does not check against
+      // MFMAs still reading their source registers, so they must not reuse those
+      asm volatile("" ::"v"(af[MI - 1]));
+#pragma unroll
+      for (int j = 0; j < NI; ++j) asm volatile("" ::"v"(bf[j]));
     }
 #pragma unroll
     for (int i = 0; i < AC; ++i) *(u32x4*)&As[cur ^ 1][arow[i]][acol[i]] = xk[i];
@@ -741,6 +747,171 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, 
           __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (f16)v), yr, off, 0, 0);
       }
     }
+}
+
+// ------------------------------------------------------------------ M <= 16 GEMV, Q4_K, 4x4x4 MFMA
+// A wave owns 64 weight rows (one per lane) and a fixed range of SPW super-blocks of
+// K; the W waves of a workgroup cover all of K for the same 64 rows and are reduced
+// through LDS in a fixed order.  v_mfma_f32_4x4x4_16b_f16 with CBSZ = 4 broadcasts
+// block ABID's A operand to all 16 blocks, so lane 4b + t holds x[token t] at k-slice
+// b of each 64-element pair chunk and one register pair feeds 16 MFMAs; each lane's
+// B operand is 4 elements of its own row.  D: lane 4b + j holds row 4b + j's sums
+// for four tokens.  Quants enter B as the exact fp16 integers 1024 + q (low nibble)
+// or 1024 + 16q (high nibble) by one v_bfi_b32 each, in element order (0, 2, 1, 3)
+// per word (x is permuted alike).  Per sub-block, with s = d*sc, c = -dmin*m:
+//   y += s'*D + (c - 1024 s')*X,   s' = s (low) or s/16 (high),
+// X = the sub-block's x sum per token, computed once per wave (ones operand) into LDS.
+constexpr int M4_MAXW = 16;
+
+template <int ABID>
+__device__ __forceinline__ f32x4 mfma4_bcast(f16x4 a, f16x4 b, f32x4 c) {   // A from block ABID
+  return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 4, ABID, 0);
+}
+template <int I, int N, class Fn>
+__device__ __forceinline__ void static_for(Fn&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>());
+    static_for<I + 1, N>(f);
+  }
+}
+
+// up to 16 waves, or 8 when the x operands need more than 64 VGPRs
+template <int TG, int SPW>
+constexpr int m4_max_threads() { return TG * SPW >= 4 ? 512 : 1024; }
+
+template <int TG, int T1, int SPW, typename YT>
+__global__ __launch_bounds__((m4_max_threads<TG, SPW>())) void k_gemv_q4k_m4(QArgs a, const f16* x, int M, YT* y, int N) {
+  // TG token groups of 4 (M <= 4 TG); T1: tokens used in each group (1 when M == 1)
+  __shared__ __attribute__((aligned(16))) float Xs[M4_MAXW][SPW * 8][TG][4];
+  __shared__ __attribute__((aligned(16))) float red[M4_MAXW][64][TG * 4];
+  const int K = a.K, KSB = K >> 8;
+  const int W = (int)(blockDim.x >> 6), wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int blk = lane >> 2, t4 = lane & 3;
+  const int sb0 = wave * SPW;                          // first super-block of this wave
+  const uint32_t rb = (uint32_t)a.rb;
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.w, (short)0, (int)((uint32_t)N * rb), ALLOY_RSRC_DW3);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)x, (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), ALLOY_RSRC_DW3);
+
+  // raw bytes of one super-block of this lane's row: header + 128 quant bytes
+  struct SB { u32x4 hd, q[8]; };
+  auto sload = [&](int rg, int s, SB& r) {   // rows past N / super-blocks past K: zero or unused
+    const uint32_t bo = (uint32_t)(rg * 64 + lane) * rb + (uint32_t)(sb0 + s) * 144u;
+    r.hd = bld16(wr, bo);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) r.q[c] = bld16(wr, bo + 16u + 16u * c);
+  };
+  SB pre;                                   // first super-block of the next row group
+  sload(blockIdx.x, 0, pre);                // in flight while x is prepared
+
+  // x operands: [group][super-block][pair] -> 4 halves (x at 4 k, order 0,2,1,3)
+  f16x4 xa[TG][SPW][4];
+#pragma unroll
+  for (int g = 0; g < TG; ++g)
+#pragma unroll
+    for (int s = 0; s < SPW; ++s)
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const int tok = 4 * g + t4;
+        const uint32_t k = (uint32_t)(sb0 + s) * 256u + 64u * p + 4u * blk;
+        // rows past M and super-blocks past K read as zero (buffer bounds)
+        const uint32_t off = (tok < M && sb0 + s < KSB) ? ((uint32_t)tok * (uint32_t)K + k) * 2u : 0x80000000u;
+        const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(xr, off, 0, 0));
+        const uint2 pv = {__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.y, v.x, 0x07060302u)};
+        xa[g][s][p] = __builtin_bit_cast(f16x4, pv);
+      }
+  // per-token sums of every sub-block of this wave's range (ones operand), into LDS
+  {
+    const f16x4 ones = {1, 1, 1, 1};
+#pragma unroll
+    for (int g = 0; g < TG; ++g)
+#pragma unroll
+      for (int s = 0; s < SPW; ++s)
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          f32x4 lo = {0.f, 0.f, 0.f, 0.f}, hi = {0.f, 0.f, 0.f, 0.f};
+          static_for<0, 8>([&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            lo = mfma4_bcast<i>(xa[g][s][p], ones, lo);
+            hi = mfma4_bcast<8 + i>(xa[g][s][p], ones, hi);
+          });
+          if (lane == 0) {
+            *(f32x4*)Xs[wave][8 * s + 2 * p][g] = lo;
+            *(f32x4*)Xs[wave][8 * s + 2 * p + 1][g] = hi;
+          }
+        }
+  }
+  __syncthreads();
+
+  const uint32_t magic = 0x64006400u;                  // fp16 1024.0 in both halves
+  const int ngroups = (N + 63) >> 6;
+  for (int rg = blockIdx.x; rg < ngroups; rg += gridDim.x) {
+    f32x4 yacc[TG];
+#pragma unroll
+    for (int g = 0; g < TG; ++g) yacc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+    SB sbuf[2];
+    sbuf[0] = pre;
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+      // the next super-block (or the next row group's first) loads during this one
+      if (s + 1 < SPW) sload(rg, s + 1, sbuf[(s + 1) & 1]);
+      else sload(rg + (int)gridDim.x, 0, pre);
+      if (sb0 + s >= KSB) continue;                    // uniform per wave
+      const u32x4 hd = sbuf[s & 1].hd;
+      const u32x4* q = sbuf[s & 1].q;
+      const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        uint32_t sc0, mn0, sc1, mn1;
+        q4k_scale_min(hd.y, hd.z, hd.w, 2 * p, sc0, mn0);       // constant sub-block
+        q4k_scale_min(hd.y, hd.z, hd.w, 2 * p + 1, sc1, mn1);
+        const float slo = d * (float)sc0, shi = d * (float)sc1 * 0.0625f;
+        const float clo = -(dmin * (float)mn0) - 1024.f * slo, chi = -(dmin * (float)mn1) - 1024.f * shi;
+        f32x4 dlo[TG], dhi[TG];
+#pragma unroll
+        for (int g = 0; g < TG; ++g) dlo[g] = dhi[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+        static_for<0, 8>([&](auto ic) {
+          constexpr int i = decltype(ic)::value;
+          const u32x4 qc = q[2 * p + (i >> 2)];
+          const uint32_t w = (i & 3) == 0 ? qc.x : (i & 3) == 1 ? qc.y : (i & 3) == 2 ? qc.z : qc.w;
+          const uint32_t w8 = w >> 8;
+          // plain expressions, not inline asm: the hazard recognizer must see these
+          // VGPR writes, which can land in registers an earlier MFMA is still reading
+          const f16x4 blo = __builtin_bit_cast(f16x4, uint2{(w & 0x000F000Fu) | magic, (w8 & 0x000F000Fu) | magic});
+          const f16x4 bhi = __builtin_bit_cast(f16x4, uint2{(w & 0x00F000F0u) | magic, (w8 & 0x00F000F0u) | magic});
+#pragma unroll
+          for (int g = 0; g < TG; ++g) {
+            dlo[g] = mfma4_bcast<i>(xa[g][s][p], blo, dlo[g]);
+            dhi[g] = mfma4_bcast<8 + i>(xa[g][s][p], bhi, dhi[g]);
+          }
+        });
+#pragma unroll
+        for (int g = 0; g < TG; ++g) {
+          const f32x4 xlo = *(const f32x4*)Xs[wave][8 * s + 2 * p][g];
+          const f32x4 xhi = *(const f32x4*)Xs[wave][8 * s + 2 * p + 1][g];
+#pragma unroll
+          for (int t = 0; t < T1; ++t) {
+            const float vlo = dlo[g][t], vhi = dhi[g][t];
+            yacc[g][t] += slo * vlo + clo * xlo[t] + shi * vhi + chi * xhi[t];
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < TG; ++g) *(f32x4*)&red[wave][lane][4 * g] = yacc[g];
+    __syncthreads();
+    // fixed-order sum over the waves: thread -> (row, token)
+    for (int e = threadIdx.x; e < 64 * TG * 4; e += blockDim.x) {
+      const int r = e / (TG * 4), tk = e - r * (TG * 4);
+      const int tokg = tk;                             // token index 4g + t
+      float v = 0.f;
+      for (int ww = 0; ww < W; ++ww) v += red[ww][r][tk];
+      const int n = rg * 64 + r;
+      if (n < N && tokg < M && ((tokg & 3) < T1)) y[(int64_t)tokg * N + n] = (YT)v;
+    }
+    __syncthreads();
+  }
 }
 
 template <template <class> class Fn, typename... Args>
@@ -933,6 +1104,53 @@ hipError_t launch_gemv_dot2(int fmt, const QArgs& a, const void* x, bool x_f32, 
   return by_fmt<GemvDot2Run>(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
 }
 
+// Q4_K M <= 16 GEMV on 4x4x4 MFMA; hipErrorNotSupported when the shape does not fit.
+static hipError_t launch_gemv_q4k_m4(const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32,
+                                     int64_t M, int64_t N, const Opts& o, hipStream_t st) {
+  if (x_f32 || M > 16 || a.K % 256 || (uint64_t)N * (uint64_t)a.rb >= (1ull << 31) ||
+      (uint64_t)M * (uint64_t)a.K * 2u >= (1ull << 31))
+    return hipErrorNotSupported;
+  const int KSB = a.K / 256;
+  const int TGn = M == 1 ? 1 : M <= 4 ? 1 : M <= 8 ? 2 : 4;
+  int spw = 1, W = KSB;
+  while (W > (TGn * spw >= 4 ? 8 : 16) && spw <= 4) { ++spw; W = (KSB + spw - 1) / spw; }
+  if (spw > 4) return hipErrorNotSupported;
+  if (TGn == 4 && spw > 2) {
+    // 16 tokens over a long K would not fit the registers: two passes of 8 tokens
+    const hipError_t e = launch_gemv_q4k_m4(a, x, x_f32, y, y_f32, 8, N, o, st);
+    if (e != hipSuccess) return e;
+    return launch_gemv_q4k_m4(a, (const f16*)x + 8 * (int64_t)a.K, x_f32,
+                              (uint8_t*)y + 8 * N * (y_f32 ? 4 : 2), y_f32, M - 8, N, o, st);
+  }
+  const int64_t ngroups = (N + 63) / 64;
+  const int64_t cap = o.grid_cap > 0 ? o.grid_cap : 1024;
+  const dim3 grid((unsigned)(ngroups < cap ? ngroups : cap)), block((unsigned)(64 * W));
+  auto go = [&](auto tg, auto t1, auto sp) -> hipError_t {
+    constexpr int TG = decltype(tg)::value, T1 = decltype(t1)::value, SP = decltype(sp)::value;
+    if (y_f32)
+      hipLaunchKernelGGL((k_gemv_q4k_m4<TG, T1, SP, float>), grid, block, 0, st, a, (const f16*)x, (int)M, (float*)y, (int)N);
+    else
+      hipLaunchKernelGGL((k_gemv_q4k_m4<TG, T1, SP, f16>), grid, block, 0, st, a, (const f16*)x, (int)M, (f16*)y, (int)N);
+    return hipGetLastError();
+  };
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  using I4 = std::integral_constant<int, 4>;
+  auto by_spw = [&](auto tg, auto t1) -> hipError_t {
+    switch (spw) {
+      case 1: return go(tg, t1, I1());
+      case 2: return go(tg, t1, I2());
+      case 3: return go(tg, t1, I3());
+      default: return go(tg, t1, I4());
+    }
+  };
+  if (M == 1) return by_spw(I1(), I1());
+  if (M <= 4) return by_spw(I1(), I4());
+  if (M <= 8) return by_spw(I2(), I4());
+  return by_spw(I4(), I4());
+}
+
 template <class F>
 struct GemvMfmaRun {
   template <int RG, typename XT>
@@ -955,6 +1173,13 @@ struct GemvMfmaRun {
 hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
                             bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;
+  // 4x4x4 kernel: measured faster than the 16x16 one up to 8 tokens, and for 16
+  // tokens only on very tall matrices
+  if (fmt == F_Q4_K && o.variant != 1 && (M <= 8 || N >= 32768 || o.variant == 5)) {
+    const hipError_t e = launch_gemv_q4k_m4(a, x, x_f32, y, y_f32, M, N, o, st);
+    if (e != hipErrorNotSupported) return e;
+    (void)hipGetLastError();
+  }
   return by_fmt<GemvMfmaRun>(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
 }
 

@@ -262,8 +262,10 @@ __device__ __forceinline__ void mlx_rows_mfma(const QArgs& a, const int64_t (&ro
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
         const uint32_t q = rin ? *(const uint32_t*)(a.w + row[w] * a.rb + (k >> 1)) : 0u;
-        const u32x4 bq = {bfi(0x000F000Fu, q, magic), bfi(0x000F000Fu, q >> 4, magic),
-                          bfi(0x000F000Fu, q >> 8, magic), bfi(0x000F000Fu, q >> 12, magic)};
+        // plain expressions, not inline asm: the hazard recognizer must see these VGPR
+        // writes, which can land in registers an earlier MFMA is still reading
+        const u32x4 bq = {(q & 0x000F000Fu) | magic, ((q >> 4) & 0x000F000Fu) | magic,
+                          ((q >> 8) & 0x000F000Fu) | magic, ((q >> 12) & 0x000F000Fu) | magic};
         dW[w] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, __builtin_bit_cast(f16x8, bq), dW[w], 0, 0, 0);
       }
       dX = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, ones, dX, 0, 0, 0);
