@@ -1104,6 +1104,161 @@ hipError_t launch_gemv_dot2(int fmt, const QArgs& a, const void* x, bool x_f32, 
   return by_fmt<GemvDot2Run>(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
 }
 
+// ------------------------------------------------------------------ M <= 16 GEMV, x-stationary 16x16x32
+// Each wave owns a fixed K range and keeps the activations of that range (16 token
+// rows, zero past M) as MFMA A operands in registers for the whole kernel; the
+// workgroup's W waves cover K for the same weight rows and are reduced through LDS
+// in a fixed order.  B = 16 weight rows x one 32-element sub-block, quants as exact
+// fp16 integers (1024 + q, high nibbles 1024 + 16q); D (lane: row l%16, tokens
+// 4(l/16)+t) is fresh per sub-block and folded in fp32 as y += s*D + c*X with the
+// sub-block's scale s, offset c (minus 1024 s) and X = sum of x over the sub-block
+// per token (computed once per wave into LDS with a ones operand).  Q4_K x is
+// permuted (0,2,1,3) per 4 elements to match the unpack order.
+template <int NS, int TT, int XS_RT, typename YT>
+__global__ __launch_bounds__(1024) void k_gemv_xs_q4k(QArgs a, const f16* x, int M, YT* y, int N) {
+  // NS: sub-blocks (of 32) per wave, a multiple of 8 (whole super-blocks); TT: tokens
+  // folded per lane (1 when M == 1, else 4); XS_RT: 16-row tiles per LDS reduction,
+  // whose weight bytes are all requested before any of them is used
+  __shared__ __attribute__((aligned(16))) float Xs[16][NS][16];
+  __shared__ __attribute__((aligned(16))) float red[16][XS_RT][64][4];
+  const int K = a.K;
+  const int W = (int)(blockDim.x >> 6), wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n16 = lane & 15, kq = lane >> 4;
+  const int k0 = wave * NS * 32;                 // first element of this wave's range
+  const int nsb = (K - k0) / 32 < NS ? (K - k0) / 32 : NS;   // sub-blocks present (multiple of 8)
+  const uint32_t rb = (uint32_t)a.rb;
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.w, (short)0, (int)((uint32_t)N * rb), ALLOY_RSRC_DW3);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)x, (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), ALLOY_RSRC_DW3);
+  // A operands: token n16, elements 32s + 8kq + (0,2,1,3, 4,6,5,7)
+  f16x8 xa[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const uint32_t off = (n16 < M && s < nsb) ? ((uint32_t)n16 * (uint32_t)K + (uint32_t)(k0 + 32 * s + 8 * kq)) * 2u
+                                              : 0x80000000u;
+    const u32x4 v = bld16(xr, off);
+    const u32x4 pv = {__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.y, v.x, 0x07060302u),
+                      __builtin_amdgcn_perm(v.w, v.z, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u)};
+    xa[s] = __builtin_bit_cast(f16x8, pv);
+  }
+  {
+    const f16x8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const f32x4 X = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[s], ones, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+      if (n16 == 0) *(f32x4*)&Xs[wave][s][4 * kq] = X;   // tokens 4kq .. 4kq+3
+    }
+  }
+  __syncthreads();
+
+  const uint32_t magic = 0x64006400u;
+  const int ntiles = (N + 15) >> 4;
+  for (int t0 = blockIdx.x * XS_RT; t0 < ntiles; t0 += gridDim.x * XS_RT) {
+    // all weight bytes of the tiles first (one memory round trip), then the math
+    u32x4 hd[XS_RT][NS / 8];
+    uint2 qw[XS_RT][NS / 8][4];
+#pragma unroll
+    for (int r = 0; r < XS_RT; ++r) {
+      const int n = (t0 + r) * 16 + n16;           // rows past N read zero
+#pragma unroll
+      for (int sb = 0; sb < NS / 8; ++sb) {        // super-blocks past K: unused
+        const uint32_t bo = (uint32_t)n * rb + (uint32_t)((k0 >> 8) + sb) * 144u;
+        hd[r][sb] = bld16(wr, bo);
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+          qw[r][sb][p] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wr, bo + 16u + 32u * p + 8u * kq, 0, 0));
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < XS_RT; ++r) {
+      f32x4 yacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int sb = 0; sb < NS / 8; ++sb) {        // super-blocks of this wave's range
+        if (sb >= nsb / 8) break;                  // uniform; keeps xa[] statically indexed
+        const u32x4 h = hd[r][sb];
+        const float d = h2f(h.x), dmin = h2f(h.x >> 16);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          uint32_t sc0, mn0, sc1, mn1;
+          q4k_scale_min(h.y, h.z, h.w, 2 * p, sc0, mn0);
+          q4k_scale_min(h.y, h.z, h.w, 2 * p + 1, sc1, mn1);
+          const float slo = d * (float)sc0, shi = d * (float)sc1 * 0.0625f;
+          const float clo = -(dmin * (float)mn0) - 1024.f * slo, chi = -(dmin * (float)mn1) - 1024.f * shi;
+          const uint32_t w0 = qw[r][sb][p].x, w1 = qw[r][sb][p].y, w08 = w0 >> 8, w18 = w1 >> 8;
+          const u32x4 blo = {(w0 & 0x000F000Fu) | magic, (w08 & 0x000F000Fu) | magic,
+                             (w1 & 0x000F000Fu) | magic, (w18 & 0x000F000Fu) | magic};
+          const u32x4 bhi = {(w0 & 0x00F000F0u) | magic, (w08 & 0x00F000F0u) | magic,
+                             (w1 & 0x00F000F0u) | magic, (w18 & 0x00F000F0u) | magic};
+          const int s = 8 * sb + 2 * p;
+          const f32x4 dlo = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[s], __builtin_bit_cast(f16x8, blo), f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          const f32x4 dhi = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[s + 1], __builtin_bit_cast(f16x8, bhi), f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          const f32x4 xl = *(const f32x4*)&Xs[wave][s][4 * kq], xh = *(const f32x4*)&Xs[wave][s + 1][4 * kq];
+#pragma unroll
+          for (int t = 0; t < TT; ++t) {
+            const float vl = dlo[t], vh = dhi[t];
+            yacc[t] += slo * vl + clo * xl[t] + shi * vh + chi * xh[t];
+          }
+        }
+      }
+      *(f32x4*)red[wave][r][lane] = yacc;
+    }
+    __syncthreads();
+    // fixed-order sum over the waves; thread -> (tile r, lane l, token slot t)
+    for (int e = threadIdx.x; e < XS_RT * 64 * 4; e += blockDim.x) {
+      const int r = e >> 8, l = (e >> 2) & 63, t = e & 3;
+      const int tok = 4 * (l >> 4) + t, n = (t0 + r) * 16 + (l & 15);
+      float v = 0.f;
+      for (int ww = 0; ww < W; ++ww) v += red[ww][r][l][t];
+      if (n < N && tok < M && (TT == 4 || t == 0)) y[(int64_t)tok * N + n] = (YT)v;
+    }
+    __syncthreads();
+  }
+}
+
+static hipError_t launch_gemv_xs_q4k(const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32,
+                                     int64_t M, int64_t N, const Opts& o, hipStream_t st) {
+  if (x_f32 || M > 16 || a.K % 256 || (uint64_t)N * (uint64_t)a.rb >= (1ull << 31) ||
+      (uint64_t)M * (uint64_t)a.K * 2u >= (1ull << 31))
+    return hipErrorNotSupported;
+  const int KS = a.K / 32;                        // sub-blocks of K
+  int ns = 8;
+  while ((KS + ns - 1) / ns > 16) ns *= 2;        // at most 16 waves
+  if (ns > 16) return hipErrorNotSupported;       // x of a longer K range would not fit
+  const int W = (KS + ns - 1) / ns;
+  const int64_t tiles = (N + 15) / 16;
+  // one 16-row tile per reduction while that still leaves <= 1024 workgroups
+  const int rt = (tiles <= 1024 || ns == 16) ? 1 : 4;   // (16 sub-blocks leave no registers)
+  const int64_t groups = (tiles + rt - 1) / rt;
+  const int64_t cap = o.grid_cap > 0 ? o.grid_cap : 1024;
+  const dim3 grid((unsigned)(groups < cap ? groups : cap)), block((unsigned)(64 * W));
+  auto go = [&](auto nsc, auto ttc) -> hipError_t {
+    constexpr int NS = decltype(nsc)::value, TT = decltype(ttc)::value;
+    auto launch = [&](auto rtc) {
+      constexpr int RT = decltype(rtc)::value;
+      if (y_f32)
+        hipLaunchKernelGGL((k_gemv_xs_q4k<NS, TT, RT, float>), grid, block, 0, st, a, (const f16*)x, (int)M, (float*)y, (int)N);
+      else
+        hipLaunchKernelGGL((k_gemv_xs_q4k<NS, TT, RT, f16>), grid, block, 0, st, a, (const f16*)x, (int)M, (f16*)y, (int)N);
+    };
+    if constexpr (NS == 8) {
+      if (rt == 4) {
+        launch(std::integral_constant<int, 4>());
+        return hipGetLastError();
+      }
+    }
+    launch(std::integral_constant<int, 1>());
+    return hipGetLastError();
+  };
+  using T1 = std::integral_constant<int, 1>;
+  using T4 = std::integral_constant<int, 4>;
+  auto by_ns = [&](auto ttc) -> hipError_t {
+    if (ns == 8) return go(std::integral_constant<int, 8>(), ttc);
+    return go(std::integral_constant<int, 16>(), ttc);
+  };
+  return M == 1 ? by_ns(T1()) : by_ns(T4());
+}
+
 // Q4_K M <= 16 GEMV on 4x4x4 MFMA; hipErrorNotSupported when the shape does not fit.
 static hipError_t launch_gemv_q4k_m4(const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32,
                                      int64_t M, int64_t N, const Opts& o, hipStream_t st) {
@@ -1173,9 +1328,14 @@ struct GemvMfmaRun {
 hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
                             bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;
-  // 4x4x4 kernel: measured faster than the 16x16 one up to 8 tokens, and for 16
-  // tokens only on very tall matrices
-  if (fmt == F_Q4_K && o.variant != 1 && (M <= 8 || N >= 32768 || o.variant == 5)) {
+  // Q4_K: x-stationary 16x16x32 kernel, except that very tall matrices with up to 8
+  // tokens run faster on the 4x4x4 broadcast kernel (fewer VGPRs, more waves)
+  if (fmt == F_Q4_K && (o.variant == 6 || (o.variant == 0 && !(N >= 32768 && M <= 8)))) {
+    const hipError_t e = launch_gemv_xs_q4k(a, x, x_f32, y, y_f32, M, N, o, st);
+    if (e != hipErrorNotSupported) return e;
+    (void)hipGetLastError();
+  }
+  if (fmt == F_Q4_K && (o.variant == 0 || o.variant == 5)) {
     const hipError_t e = launch_gemv_q4k_m4(a, x, x_f32, y, y_f32, M, N, o, st);
     if (e != hipErrorNotSupported) return e;
     (void)hipGetLastError();

@@ -122,8 +122,9 @@ def test_gemv_mfma(dev, fmt, M):
         y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=rg << 28).cpu().numpy()
         check(y, x, wt.W, f"{fmt} gemv_mfma M={M} rg={rg}")
     if fmt == "q4_k" and M <= 16:
-        # both kernels explicitly: 1 = 16x16x32 tiles, 5 = 4x4x4 broadcast (Q4_K)
-        for variant in (1, 5):
+        # every kernel explicitly: 1 = 16x16x32 tiles, 5 = 4x4x4 broadcast (Q4_K),
+        # 6 = x-stationary 16x16x32 (Q4_K)
+        for variant in (1, 5, 6):
             y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=variant << 36).cpu().numpy()
             check(y, x, wt.W, f"{fmt} gemv_mfma M={M} variant={variant}")
 
