@@ -4,6 +4,7 @@
 #include <type_traits>
 
 #include "launch.h"
+#include "xs.h"
 
 namespace alloy {
 
@@ -1325,9 +1326,41 @@ struct GemvMfmaRun {
   }
 };
 
+// M <= 16 on the generic x-stationary kernel (Q4_K, MLX with a power-of-two group
+// size); hipErrorNotSupported when the format or shape does not fit it.
+static hipError_t launch_gemv_xs(int fmt, const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32,
+                                 int64_t M, int64_t N, const Opts& o, hipStream_t st) {
+  if (x_f32 || M > 16 || N >= (1ll << 31) || (uint64_t)M * (uint64_t)a.K * 2u >= (1ull << 31))
+    return hipErrorNotSupported;
+  XsJob j{};
+  j.a = a;
+  j.x = (const f16*)x;
+  j.xbytes = (uint32_t)(M * a.K * 2);
+  j.xld = a.K;
+  j.M = (int)M;
+  j.N = (int)N;
+  j.y = y;
+  j.y_f32 = y_f32;
+  const int64_t cap = o.grid_cap > 0 ? o.grid_cap : 1024;
+  if (fmt == F_Q4_K) return launch_xs<XsQ4K, 0>(j, 0, cap, o.row_groups, st);
+  if (fmt != F_MLX || a.gs < 32 || (a.gs & (a.gs - 1))) return hipErrorNotSupported;
+  j.sb = (uint32_t)(a.K / a.gs * 2);
+  switch (a.gs) {
+    case 32: return launch_xs<XsMLX<0>, 0>(j, 0, cap, o.row_groups, st);
+    case 64: return launch_xs<XsMLX<1>, 0>(j, 0, cap, o.row_groups, st);
+    case 128: return launch_xs<XsMLX<2>, 0>(j, 0, cap, o.row_groups, st);
+    default: return a.gs == 256 ? launch_xs<XsMLX<3>, 0>(j, 0, cap, o.row_groups, st) : hipErrorNotSupported;
+  }
+}
+
 hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
                             bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;
+  if (o.variant == 7 || (o.variant == 0 && fmt == F_MLX)) {
+    const hipError_t e = launch_gemv_xs(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
+    if (e != hipErrorNotSupported) return e;
+    (void)hipGetLastError();
+  }
   // Q4_K: x-stationary 16x16x32 kernel, except that very tall matrices with up to 8
   // tokens run faster on the 4x4x4 broadcast kernel (fewer VGPRs, more waves)
   if (fmt == F_Q4_K && (o.variant == 6 || (o.variant == 0 && !(N >= 32768 && M <= 8)))) {

@@ -11,6 +11,10 @@ namespace alloy {
 enum Fmt : int { F_Q8_0 = 0, F_Q5_0 = 1, F_Q4_K = 2, F_Q6_K = 3, F_MLX = 4, F_Q8_0S = 5, F_Q5_0S = 6 };
 enum Path : int { P_AUTO = 0, P_GEMV = 1, P_GEMV_MFMA = 2, P_GEMM = 3 };
 
+// Routed-expert column tile record (ints): expert, first expert-sorted position,
+// route count (<= 16), 0, then the token index of each of the 16 route slots.
+constexpr int kTileInts = 20;
+
 // Launch-shape knobs (0 = automatic choice).
 struct Opts {
   int lanes_per_row = 0;   // dot2 GEMV: threads cooperating on one row (multiple of 16, <= 256)

@@ -5,19 +5,26 @@
 //                   (reference: packages/alloy-metal/src/alloy/std/moe.py:31-79)
 //   2. k_sort       one workgroup: stable counting sort of the T*k routes by expert
 //                   (order within an expert = route order), inverse permutation, and
-//                   a list of column tiles (<= 16 routes of one expert each)
+//                   column tile records (<= 16 routes of one expert each, with the
+//                   token of every route slot)
 //                   (reference role: moe.py:504-735, without padding rows)
-//   3. k_gate_up    per (tile, 16 gate rows): gathered exact MFMA GEMV over the
+//                   Up to kFusedTokens tokens, 1 and 2 run as one workgroup
+//                   (k_route_sort) with the picks kept in LDS.
+//   3. gate/up      per (tile, 16 gate rows): gathered exact MFMA GEMV over the
 //                   tile's tokens (quants as fp16 integers, group scale and bias
 //                   applied in fp32), h = silu(G_e x) * (U_e x) stored fp16 per
 //                   sorted route
 //                   (reference role: moe.py:82-135, 225-306; fused rows [0:I] gate,
 //                   [I:2I] up, packages/alloy-server/src/alloy_server/models/qwen3_5.py:383-385)
-//   4. k_down       per (tile, 16 hidden rows): D_e h -> fp32 partial per sorted route
+//   4. down         per (tile, 16 hidden rows): D_e h -> fp32 partial per sorted route
+//                   3 and 4 run on the x-stationary kernel (xs.h) when H and I are
+//                   multiples of 256 and the group size a power of two, else on
+//                   k_gate_up / k_down below.
 //   5. k_combine    y[t] = sum_s w[t,s] * partial[inv[t,s]] in slot order
 //                   (reference role: moe.py:479-501, fixed-order combine)
 // Each expert's weights are read once per column tile of its routed tokens.
 #include "moe.h"
+#include "xs.h"
 
 namespace alloy {
 
@@ -32,7 +39,7 @@ MoeLayout moe_layout(int64_t T, int E, int top_k, int64_t H, int64_t I) {
   L.wts = o; o = align256(o + 4 * (size_t)L.R);
   L.sorted = o; o = align256(o + 4 * (size_t)L.R);
   L.inv = o; o = align256(o + 4 * (size_t)L.R);
-  L.tiles = o; o = align256(o + 16 * (size_t)L.max_tiles);
+  L.tiles = o; o = align256(o + 4 * kTileInts * (size_t)L.max_tiles);
   L.ntiles = o; o = align256(o + 4);
   L.h = o; o = align256(o + 2 * (size_t)L.R * (size_t)I);
   L.part = o; o = align256(o + 4 * (size_t)L.R * (size_t)H);
@@ -41,13 +48,13 @@ MoeLayout moe_layout(int64_t T, int E, int top_k, int64_t H, int64_t I) {
 }
 
 // ------------------------------------------------------------------ router
+// One wave routes token t: top-k of the E logits (ties -> lowest index, NaN never
+// wins over a number), then the softmax over the k picks in pick order.  Pick k's
+// value and index end in lane k; lane 0 writes idx / wts (and ridx, when given).
 template <int VPL>
-__global__ __launch_bounds__(64) void k_router(const float* logits, int32_t* idx, float* wts, int E,
-                                               int top_k) {
-  __shared__ float sv[kMoeMaxTopK];
-  __shared__ int si[kMoeMaxTopK];
-  const int64_t t = blockIdx.x;
-  const int lane = threadIdx.x;
+__device__ __forceinline__ void route_token(const float* logits, int64_t t, int E, int top_k,
+                                            int32_t* idx, float* wts, int* ridx) {
+  const int lane = threadIdx.x & 63;
   float v[VPL];
   uint32_t used = 0;
 #pragma unroll
@@ -56,12 +63,14 @@ __global__ __launch_bounds__(64) void k_router(const float* logits, int32_t* idx
     float f = -INFINITY;
     if (e < E) {
       f = logits[t * E + e];
-      if (f != f) f = -INFINITY;   // NaN never wins over a number
+      if (f != f) f = -INFINITY;
     } else {
       used |= 1u << j;
     }
     v[j] = f;
   }
+  float myv = -INFINITY;
+  int myi = 0;
   for (int k = 0; k < top_k; ++k) {
     float bv = -INFINITY;
     int bi = 0x7FFFFFFF;
@@ -77,18 +86,22 @@ __global__ __launch_bounds__(64) void k_router(const float* logits, int32_t* idx
       if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
     }
     if ((bi & 63) == lane) used |= 1u << (bi >> 6);
-    if (lane == 0) { sv[k] = bv; si[k] = bi; }
+    if (lane == k) { myv = bv; myi = bi; }
   }
-  __syncthreads();
-  if (lane == 0) {
-    const float m0 = sv[0];
-    float sum = 0.f;
-    for (int k = 0; k < top_k; ++k) sum += expf(sv[k] - m0);
-    for (int k = 0; k < top_k; ++k) {
-      idx[t * top_k + k] = si[k];
-      wts[t * top_k + k] = expf(sv[k] - m0) / sum;
-    }
+  const float m0 = __shfl(myv, 0, 64);
+  float sum = 0.f;
+  for (int k = 0; k < top_k; ++k) sum += expf(__shfl(myv, k, 64) - m0);   // pick order
+  if (lane < top_k) {
+    idx[t * top_k + lane] = myi;
+    wts[t * top_k + lane] = expf(myv - m0) / sum;
+    if (ridx) ridx[t * top_k + lane] = myi;
   }
+}
+
+template <int VPL>
+__global__ __launch_bounds__(64) void k_router(const float* logits, int32_t* idx, float* wts, int E,
+                                               int top_k) {
+  route_token<VPL>(logits, blockIdx.x, E, top_k, idx, wts, nullptr);
 }
 
 hipError_t launch_router(const float* logits, int32_t* idx, float* w, int64_t T, int E, int top_k,
@@ -133,13 +146,19 @@ __device__ int block_excl_scan(int v, int* scratch, int* total) {
 }
 
 constexpr int kSortWaves = 16;
+constexpr int kFusedTokens = kSortWaves;   // tokens the one-workgroup router + sort takes
 
-// dynamic LDS: wcnt[kSortWaves][E] ints + 64 ints scratch
-__global__ __launch_bounds__(1024) void k_sort(const int32_t* idx, int R, int E, int32_t* sorted,
-                                               int32_t* inv, int32_t* tiles, int32_t* ntiles) {
-  extern __shared__ int lds[];
+// Stable counting sort of the R routes by expert (order within an expert = route
+// order) by one 1024-thread workgroup: sorted (position -> route), inv (route ->
+// position) and the column tile records (kTileInts ints each, <= 16 routes of one
+// expert, token index = route / top_k per slot).  idx may point to LDS or global
+// memory.  lds: wcnt[kSortWaves][E] + eoff[E] + etb[E] + 64 scratch ints.
+__device__ void sort_routes(const int* idx, int R, int E, int top_k, int* lds, int32_t* sorted,
+                            int32_t* inv, int32_t* tiles, int32_t* ntiles) {
   int* wcnt = lds;                        // [w * E + e]
-  int* scratch = lds + kSortWaves * E;
+  int* eoff = lds + kSortWaves * E;       // first sorted position of expert e
+  int* etb = eoff + E;                    // first tile of expert e
+  int* scratch = etb + E;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   for (int i = tid; i < kSortWaves * E; i += 1024) wcnt[i] = 0;
   __syncthreads();
@@ -156,6 +175,8 @@ __global__ __launch_bounds__(1024) void k_sort(const int32_t* idx, int R, int E,
   int ntot;
   const int tb = block_excl_scan(tid < E ? (tot + kMoeColTile - 1) / kMoeColTile : 0, scratch, &ntot);
   if (tid < E) {
+    eoff[tid] = off;
+    etb[tid] = tb;
     int base = off;
     for (int w = 0; w < kSortWaves; ++w) {
       const int c = wcnt[w * E + tid];
@@ -181,6 +202,8 @@ __global__ __launch_bounds__(1024) void k_sort(const int32_t* idx, int R, int E,
       const int pos = wcnt[wave * E + e] + __popcll(peers & lt);
       sorted[pos] = r;
       inv[r] = pos;
+      const int q = pos - eoff[e];
+      tiles[kTileInts * (etb[e] + q / kMoeColTile) + 4 + q % kMoeColTile] = r / top_k;
     }
     __builtin_amdgcn_wave_barrier();
     if (valid && (peers >> lane) == 1ull) wcnt[wave * E + e] += __popcll(peers);
@@ -188,15 +211,36 @@ __global__ __launch_bounds__(1024) void k_sort(const int32_t* idx, int R, int E,
   }
   if (tid < E) {
     const int n = tot;
-    for (int j = 0; 16 * j < n; ++j) {
-      int32_t* tp = tiles + 4 * (tb + j);
+    for (int j = 0; kMoeColTile * j < n; ++j) {
+      int32_t* tp = tiles + kTileInts * (tb + j);
       tp[0] = tid;
-      tp[1] = off + 16 * j;
-      tp[2] = n - 16 * j < 16 ? n - 16 * j : 16;
+      tp[1] = off + kMoeColTile * j;
+      tp[2] = n - kMoeColTile * j < kMoeColTile ? n - kMoeColTile * j : kMoeColTile;
       tp[3] = 0;
     }
   }
   if (tid == 0) *ntiles = ntot;
+}
+
+__global__ __launch_bounds__(1024) void k_sort(const int32_t* idx, int R, int E, int top_k, int32_t* sorted,
+                                               int32_t* inv, int32_t* tiles, int32_t* ntiles) {
+  extern __shared__ int lds[];
+  sort_routes(idx, R, E, top_k, lds, sorted, inv, tiles, ntiles);
+}
+
+// Router and sort in one workgroup (T <= kFusedTokens): wave w routes token w; the
+// expert picks stay in LDS for the sort.
+// lds: ridx[R] + the sort's LDS.
+template <int VPL>
+__global__ __launch_bounds__(1024) void k_route_sort(const float* logits, int64_t T, int E, int top_k,
+                                                     int32_t* idx, float* wts, int32_t* sorted,
+                                                     int32_t* inv, int32_t* tiles, int32_t* ntiles) {
+  extern __shared__ int lds[];
+  const int R = (int)T * top_k;
+  int* ridx = lds;
+  for (int64_t t = threadIdx.x >> 6; t < T; t += kSortWaves) route_token<VPL>(logits, t, E, top_k, idx, wts, ridx);
+  __syncthreads();
+  sort_routes(ridx, R, E, top_k, lds + ((R + 63) & ~63), sorted, inv, tiles, ntiles);
 }
 
 // ------------------------------------------------------------------ grouped GEMVs
@@ -287,7 +331,7 @@ __global__ __launch_bounds__(256) void k_gate_up(QArgs gu, const f16* x, const i
   __shared__ float red[3][2][64][4];
   const int tile = blockIdx.x;
   if (tile >= *ntiles) return;
-  const int e = tiles[4 * tile], p0 = tiles[4 * tile + 1], cnt = tiles[4 * tile + 2];
+  const int e = tiles[kTileInts * tile], p0 = tiles[kTileInts * tile + 1], cnt = tiles[kTileInts * tile + 2];
   const int i0 = blockIdx.y * 16;
   const int K = gu.K;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -318,7 +362,7 @@ __global__ __launch_bounds__(256) void k_down(QArgs dn, const f16* h, const int3
   __shared__ float red[3][1][64][4];
   const int tile = blockIdx.x;
   if (tile >= *ntiles) return;
-  const int e = tiles[4 * tile], p0 = tiles[4 * tile + 1], cnt = tiles[4 * tile + 2];
+  const int e = tiles[kTileInts * tile], p0 = tiles[kTileInts * tile + 1], cnt = tiles[kTileInts * tile + 2];
   const int j0 = blockIdx.y * 16;
   const int K = dn.K;   // = I
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -352,6 +396,58 @@ __global__ __launch_bounds__(256) void k_combine(const float* part, const int32_
   y[t * H + j] = acc;
 }
 
+// gate/up and down on the x-stationary kernel (K of both a multiple of 256, group
+// size a power of two); hipErrorNotSupported otherwise, before anything is launched.
+template <int GSH>
+static hipError_t experts_xs(const MoeArgs& m, const MoeLayout& L, const int32_t* sorted,
+                             const int32_t* tiles, const int32_t* ntiles, f16* h, float* part,
+                             hipStream_t st) {
+  XsJob g{};
+  g.a = m.gu;
+  g.sb = (uint32_t)(m.H / m.gu.gs * 2);
+  g.x = m.x;
+  g.xbytes = (uint32_t)(m.T * m.H * 2);
+  g.xld = (int)m.H;
+  g.M = (int)(m.T < 16 ? m.T : 16);   // routes per tile <= tokens
+  g.N = (int)m.I;
+  g.tiles = tiles;
+  g.ntiles = ntiles;
+  g.h = h;
+  XsJob d = g;
+  d.a = m.dn;
+  d.sb = (uint32_t)(m.I / m.dn.gs * 2);
+  d.x = h;
+  d.xbytes = (uint32_t)(L.R * m.I * 2);
+  d.xld = (int)m.I;
+  d.N = (int)m.H;
+  d.part = part;
+  hipError_t e = launch_xs<XsMLX<GSH>, 1>(g, L.max_tiles, 0, 0, st);
+  if (e != hipSuccess) return e;
+  e = launch_xs<XsMLX<GSH>, 2>(d, L.max_tiles, 0, 0, st);
+  // the gate/up launch has been enqueued: a down launch that does not fit is an error
+  return e == hipErrorNotSupported ? hipErrorInvalidValue : e;
+}
+
+static hipError_t launch_experts_xs(const MoeArgs& m, const MoeLayout& L, const int32_t* sorted,
+                                    const int32_t* tiles, const int32_t* ntiles, f16* h, float* part,
+                                    hipStream_t st) {
+  const int gs = m.gu.gs;
+  if (m.H % 256 || m.I % 256 || m.H > 4096 || m.I > 8192 || (gs & (gs - 1)) || gs < 32 || gs > 4096 ||
+      L.max_tiles > 65535 || (uint64_t)m.T * m.H * 2 >= (1ull << 31) || (uint64_t)L.R * m.I * 2 >= (1ull << 31) ||
+      (uint64_t)(2 * m.I + 16) * m.gu.rb >= (1ull << 31) || (uint64_t)(m.H + 16) * m.dn.rb >= (1ull << 31))
+    return hipErrorNotSupported;
+  switch (gs) {
+    case 32: return experts_xs<0>(m, L, sorted, tiles, ntiles, h, part, st);
+    case 64: return experts_xs<1>(m, L, sorted, tiles, ntiles, h, part, st);
+    case 128: return experts_xs<2>(m, L, sorted, tiles, ntiles, h, part, st);
+    case 256: return experts_xs<3>(m, L, sorted, tiles, ntiles, h, part, st);
+    case 512: return experts_xs<4>(m, L, sorted, tiles, ntiles, h, part, st);
+    case 1024: return experts_xs<5>(m, L, sorted, tiles, ntiles, h, part, st);
+    case 2048: return experts_xs<6>(m, L, sorted, tiles, ntiles, h, part, st);
+    default: return experts_xs<7>(m, L, sorted, tiles, ntiles, h, part, st);
+  }
+}
+
 hipError_t launch_mlx_moe(const MoeArgs& m, const MoeLayout& L, hipStream_t st) {
   int32_t* idx = (int32_t*)(m.ws + L.idx);
   float* wts = (float*)(m.ws + L.wts);
@@ -361,21 +457,45 @@ hipError_t launch_mlx_moe(const MoeArgs& m, const MoeLayout& L, hipStream_t st) 
   int32_t* ntiles = (int32_t*)(m.ws + L.ntiles);
   f16* h = (f16*)(m.ws + L.h);
   float* part = (float*)(m.ws + L.part);
-  hipError_t e = launch_router(m.logits, idx, wts, m.T, m.E, m.top_k, st);
-  if (e != hipSuccess) return e;
-  const size_t shm = (size_t)(kSortWaves * m.E + 64) * sizeof(int);
-  if (shm > 65536) {
-    e = hipFuncSetAttribute((const void*)k_sort, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+  hipError_t e = hipSuccess;
+  const size_t sort_lds = (size_t)(kSortWaves * m.E + 2 * m.E + 64) * sizeof(int);
+  if (m.T <= kFusedTokens) {
+    const size_t shm = sort_lds + (size_t)((L.R + 63) & ~63) * sizeof(int);
+    auto fused = [&](auto kern) -> hipError_t {
+      if (shm > 65536) {
+        const hipError_t r = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+        if (r != hipSuccess) return r;
+      }
+      hipLaunchKernelGGL(kern, dim3(1), dim3(1024), shm, st, m.logits, m.T, m.E, m.top_k, idx, wts, sorted, inv,
+                         tiles, ntiles);
+      return hipGetLastError();
+    };
+    const int vpl = (m.E + 63) / 64;
+    e = vpl <= 2 ? fused(k_route_sort<2>) : vpl <= 4 ? fused(k_route_sort<4>)
+      : vpl <= 8 ? fused(k_route_sort<8>) : fused(k_route_sort<16>);
     if (e != hipSuccess) return e;
+  } else {
+    e = launch_router(m.logits, idx, wts, m.T, m.E, m.top_k, st);
+    if (e != hipSuccess) return e;
+    if (sort_lds > 65536) {
+      e = hipFuncSetAttribute((const void*)k_sort, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sort_lds);
+      if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(k_sort, dim3(1), dim3(1024), sort_lds, st, idx, (int)L.R, m.E, m.top_k, sorted, inv, tiles,
+                       ntiles);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(k_sort, dim3(1), dim3(1024), shm, st, idx, (int)L.R, m.E, sorted, inv, tiles, ntiles);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(k_gate_up, dim3((unsigned)L.max_tiles, (unsigned)((m.I + 15) / 16)), dim3(256), 0, st,
-                     m.gu, m.x, sorted, tiles, ntiles, h, m.top_k, (int)m.I);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(k_down, dim3((unsigned)L.max_tiles, (unsigned)((m.H + 15) / 16)), dim3(256), 0, st,
-                     m.dn, h, tiles, ntiles, part, (int)m.H);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+  e = launch_experts_xs(m, L, sorted, tiles, ntiles, h, part, st);
+  if (e == hipErrorNotSupported) {
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(k_gate_up, dim3((unsigned)L.max_tiles, (unsigned)((m.I + 15) / 16)), dim3(256), 0, st,
+                       m.gu, m.x, sorted, tiles, ntiles, h, m.top_k, (int)m.I);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_down, dim3((unsigned)L.max_tiles, (unsigned)((m.H + 15) / 16)), dim3(256), 0, st,
+                       m.dn, h, tiles, ntiles, part, (int)m.H);
+    e = hipGetLastError();
+  }
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_combine, dim3((unsigned)m.T, (unsigned)((m.H + 255) / 256)), dim3(256), 0, st,
                      part, inv, wts, m.y, m.top_k, (int)m.H);
   return hipGetLastError();

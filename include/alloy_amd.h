@@ -74,7 +74,8 @@ typedef enum {
  *   thread of the v_dot2 GEMV (2, 3 or 4), bits 36-39 the kernel variant (0
  *   automatic).  GEMV: 1 register ring with an LDS row combine, 2 LDS-staged row
  *   tiles, 3 wave rows with buffer loads and DPP reductions.  MFMA GEMV (M <= 16):
- *   1 16x16x32 tiles, 5 Q4_K 4x4x4 broadcast tiles.  GEMM: 1 generic 128x128
+ *   1 16x16x32 tiles, 5 Q4_K 4x4x4 broadcast tiles, 6 Q4_K x-stationary tiles,
+ *   7 x-stationary tiles of any format that has them.  GEMM: 1 generic 128x128
  *   tiles, 4 / 5 / 6 Q4_K tiles of 256x256 / 128x256 / 128x128.
  * No reference counterpart as a single op: the reference dispatches per format
  * (packages/alloy-torch/src/alloy_torch/ops/linalg.py:346-739); the named entry

@@ -121,10 +121,10 @@ def test_gemv_mfma(dev, fmt, M):
     for rg in (1, 2):
         y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=rg << 28).cpu().numpy()
         check(y, x, wt.W, f"{fmt} gemv_mfma M={M} rg={rg}")
-    if fmt == "q4_k" and M <= 16:
+    if fmt in ("q4_k", "mlx_q4") and M <= 16:
         # every kernel explicitly: 1 = 16x16x32 tiles, 5 = 4x4x4 broadcast (Q4_K),
-        # 6 = x-stationary 16x16x32 (Q4_K)
-        for variant in (1, 5, 6):
+        # 6 = x-stationary 16x16x32 (Q4_K), 7 = generic x-stationary (Q4_K, MLX)
+        for variant in ((1, 5, 6, 7) if fmt == "q4_k" else (1, 7)):
             y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=variant << 36).cpu().numpy()
             check(y, x, wt.W, f"{fmt} gemv_mfma M={M} variant={variant}")
 
@@ -199,3 +199,16 @@ def test_q8_0_config1(dev):
 @pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 14336), (14336, 4096)])
 def test_q4_k_prefill_shapes(dev, M, K, N):
     _sampled("q4_k", N, K, M, dev, seed=M + K + N, path="gemm")
+
+
+@pytest.mark.parametrize("gs", [32, 128, 256])
+def test_gemv_xs_mlx_group_sizes(dev, gs):
+    # x-stationary MLX GEMV with 8, 2 and 1 groups per 256-element unit
+    rng = np.random.default_rng(gs)
+    N, K, M = 150, 2048, 5
+    wt = Weight("mlx_q4", N, K, rng, dev, gs=gs)
+    x = synth.numpy_x(M, K, rng)
+    xt = torch.from_numpy(x).to(dev)
+    for variant in (0, 7):
+        y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=variant << 36).cpu().numpy()
+        check(y, x, wt.W, f"mlx_q4 gs={gs} gemv_mfma M={M} variant={variant}")

@@ -69,6 +69,13 @@ def test_moe_small(dev, T):
     run_case(dev, T, E=8, k=2, H=256, I=128, gs=64, seed=T)
 
 
+@pytest.mark.parametrize("gs", [32, 64, 128, 256])
+def test_moe_group_sizes(dev, gs):
+    # K of gate/up 512 and of down 256: the x-stationary expert kernels with 2 and 1
+    # waves; 21 tokens x top-2 over 8 experts gives full and partial column tiles
+    run_case(dev, 21, E=8, k=2, H=512, I=256, gs=gs, seed=gs)
+
+
 @pytest.mark.parametrize("T", [1, 16, 256])
 def test_moe_config5(dev, T):
     # 128 experts, top-8, H=2048, I=768, gs=64; check up to 12 tokens against the oracle
