@@ -9,12 +9,12 @@ ctypes.  Importing the package registers the ``torch.ops.alloy.*`` ops.
 from . import formats, synth
 from ._lib import LIB_PATH, LibraryMissing, lib
 from .modules import (GGUFQ4_KLinear, GGUFQ5_0Linear, GGUFQ6_KLinear, GGUFQ8_0Linear, GGUFQuantLinear,
-                      MLXMoeExperts, MLXQ4Linear)
-from .ops import dequant, mlx_moe_routed, moe_workspace_bytes, qmm, router_topk
+                      GGUFQwen35MoeBlock, GGUFQwen35MoeExperts, MLXMoeExperts, MLXQ4Linear)
+from .ops import dequant, gguf_moe_routed, mlx_moe_routed, moe_workspace_bytes, qmm, router_topk
 
 __all__ = [
     "LIB_PATH", "LibraryMissing", "lib", "formats", "synth",
     "GGUFQuantLinear", "GGUFQ8_0Linear", "GGUFQ5_0Linear", "GGUFQ4_KLinear", "GGUFQ6_KLinear",
-    "MLXQ4Linear", "MLXMoeExperts",
-    "qmm", "dequant", "router_topk", "mlx_moe_routed", "moe_workspace_bytes",
+    "MLXQ4Linear", "MLXMoeExperts", "GGUFQwen35MoeExperts", "GGUFQwen35MoeBlock",
+    "qmm", "dequant", "router_topk", "mlx_moe_routed", "gguf_moe_routed", "moe_workspace_bytes",
 ]

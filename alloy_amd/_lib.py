@@ -52,6 +52,7 @@ SIGNATURES = {
     "alloy_moe_router_topk": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _vp]),
     "alloy_moe_workspace_bytes": (_sz, [_i64, _i32, _i32, _i64, _i64]),
     "alloy_mlx_moe_routed": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _i64, _vp, _sz, _vp, _vp]),
+    "alloy_gguf_moe_routed": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i64, _i64, _i64, _vp, _sz, _vp, _vp]),
     "alloy_last_error": (ctypes.c_char_p, []),
     "alloy_version": (ctypes.c_char_p, []),
 }

@@ -248,4 +248,33 @@ alloy_status alloy_mlx_moe_routed(const void* hidden, const float* logits, const
   return hip_status(alloy::launch_mlx_moe(m, L, (hipStream_t)stream), "moe launch");
 }
 
+alloy_status alloy_gguf_moe_routed(const void* hidden, const float* logits, const void* gate_up_blocks,
+                                   const void* down_qweight, int32_t E, int32_t top_k, int64_t T, int64_t H,
+                                   int64_t I, void* ws, size_t ws_bytes, float* y, void* stream) {
+  if (T < 0) return fail(ALLOY_E_SHAPE, "negative T");
+  if (E <= 0 || E > alloy::kMoeMaxExperts) return fail(ALLOY_E_UNSUPPORTED, "num_experts %d outside [1, %d]", E, alloy::kMoeMaxExperts);
+  if (top_k <= 0 || top_k > E || top_k > alloy::kMoeMaxTopK) return fail(ALLOY_E_SHAPE, "top_k %d invalid for %d experts", top_k, E);
+  if (T * top_k > alloy::kMoeMaxRoutes) return fail(ALLOY_E_UNSUPPORTED, "T*top_k=%lld exceeds %d", (long long)(T * top_k), alloy::kMoeMaxRoutes);
+  if (H <= 0 || I <= 0 || H % 256 || I % 256)
+    return fail(ALLOY_E_SHAPE, "hidden %lld and moe_intermediate %lld must be positive multiples of 256", (long long)H, (long long)I);
+  const alloy::MoeLayout L = alloy::moe_layout(T, E, top_k, H, I);
+  if (!alloy::gguf_moe_supported(T, H, I, L))
+    return fail(ALLOY_E_UNSUPPORTED, "gguf_moe_routed: H=%lld I=%lld T=%lld beyond the supported sizes (H, I <= 4096)",
+                (long long)H, (long long)I, (long long)T);
+  if (T == 0) return ALLOY_OK;
+  if (!hidden || !logits || !gate_up_blocks || !down_qweight || !y || !ws) return fail(ALLOY_E_ARG, "null pointer");
+  if (!aligned(hidden, 16) || !aligned(gate_up_blocks, 16) || !aligned(down_qweight, 2) || !aligned(ws, 256))
+    return fail(ALLOY_E_ALIGN, "hidden/gate_up_blocks must be 16-byte, down_qweight 2-byte and workspace 256-byte aligned");
+  if (ws_bytes < L.total) return fail(ALLOY_E_SHAPE, "workspace %zu bytes < required %zu", ws_bytes, L.total);
+  alloy::MoeArgs m{};
+  m.x = (const f16*)hidden;
+  m.logits = logits;
+  m.gu = QArgs{(const uint8_t*)gate_up_blocks, nullptr, nullptr, nullptr, H / 256 * 144, 32, (int32_t)H};
+  m.dn = QArgs{(const uint8_t*)down_qweight, nullptr, nullptr, nullptr, I / 256 * 210, 32, (int32_t)I};
+  m.E = E; m.top_k = top_k; m.T = T; m.H = H; m.I = I;
+  m.ws = (uint8_t*)ws;
+  m.y = y;
+  return hip_status(alloy::launch_gguf_moe(m, L, (hipStream_t)stream), "gguf moe launch");
+}
+
 }  // extern "C"

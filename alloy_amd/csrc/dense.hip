@@ -1326,8 +1326,8 @@ struct GemvMfmaRun {
   }
 };
 
-// M <= 16 on the generic x-stationary kernel (Q4_K, MLX with a power-of-two group
-// size); hipErrorNotSupported when the format or shape does not fit it.
+// M <= 16 on the generic x-stationary kernel (Q4_K, Q6_K, MLX with a power-of-two
+// group size); hipErrorNotSupported when the format or shape does not fit it.
 static hipError_t launch_gemv_xs(int fmt, const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32,
                                  int64_t M, int64_t N, const Opts& o, hipStream_t st) {
   if (x_f32 || M > 16 || N >= (1ll << 31) || (uint64_t)M * (uint64_t)a.K * 2u >= (1ull << 31))
@@ -1343,6 +1343,7 @@ static hipError_t launch_gemv_xs(int fmt, const QArgs& a, const void* x, bool x_
   j.y_f32 = y_f32;
   const int64_t cap = o.grid_cap > 0 ? o.grid_cap : 1024;
   if (fmt == F_Q4_K) return launch_xs<XsQ4K, 0>(j, 0, cap, o.row_groups, st);
+  if (fmt == F_Q6_K) return launch_xs<XsQ6K, 0>(j, 0, cap, o.row_groups, st);
   if (fmt != F_MLX || a.gs < 32 || (a.gs & (a.gs - 1))) return hipErrorNotSupported;
   j.sb = (uint32_t)(a.K / a.gs * 2);
   switch (a.gs) {

@@ -1,4 +1,5 @@
-// Routed-expert MoE over MLX 4-bit experts: workspace layout and launchers.
+// Routed-expert MoE over MLX 4-bit or GGUF (Q4_K gate/up, Q6_K down) experts:
+// workspace layout and launchers.
 #pragma once
 #include "launch.h"
 
@@ -19,7 +20,7 @@ struct MoeLayout {
   size_t inv = 0;         // i32[R]   route -> expert-sorted position
   size_t tiles = 0;       // i32[max_tiles][4]: expert, first sorted position, count, pad
   size_t ntiles = 0;      // i32[1]   number of valid tiles
-  size_t h = 0;           // f16[R][I]  silu(gate) * up per sorted position
+  size_t h = 0;           // f32[R][I]  silu(gate) * up per sorted position
   size_t part = 0;        // f32[R][H]  down projection per sorted position
   size_t total = 0;
 };
@@ -40,5 +41,8 @@ struct MoeArgs {
 hipError_t launch_router(const float* logits, int32_t* idx, float* w, int64_t T, int E, int top_k,
                          hipStream_t st);
 hipError_t launch_mlx_moe(const MoeArgs& m, const MoeLayout& L, hipStream_t st);
+// GGUF experts: gate/up Q4_K (gu.rb = H/256*144), down Q6_K (dn.rb = I/256*210).
+bool gguf_moe_supported(int64_t T, int64_t H, int64_t I, const MoeLayout& L);
+hipError_t launch_gguf_moe(const MoeArgs& m, const MoeLayout& L, hipStream_t st);
 
 }  // namespace alloy

@@ -1,4 +1,5 @@
-// Routed-expert MoE over MLX 4-bit experts for gfx950.
+// Routed-expert MoE over MLX 4-bit and GGUF (Q4_K gate/up, Q6_K down) experts for
+// gfx950.
 //
 // Pipeline (all on the caller's stream, deterministic, no float atomics):
 //   1. k_router     per token: top-k logits (ties -> lowest index), softmax over k
@@ -12,14 +13,16 @@
 //                   (k_route_sort) with the picks kept in LDS.
 //   3. gate/up      per (tile, 16 gate rows): gathered exact MFMA GEMV over the
 //                   tile's tokens (quants as fp16 integers, group scale and bias
-//                   applied in fp32), h = silu(G_e x) * (U_e x) stored fp16 per
+//                   applied in fp32), h = silu(G_e x) * (U_e x) stored fp32 per
 //                   sorted route
 //                   (reference role: moe.py:82-135, 225-306; fused rows [0:I] gate,
 //                   [I:2I] up, packages/alloy-server/src/alloy_server/models/qwen3_5.py:383-385)
 //   4. down         per (tile, 16 hidden rows): D_e h -> fp32 partial per sorted route
+//                   (h enters the MFMA as fp16 after a per-token power-of-two scale)
 //                   3 and 4 run on the x-stationary kernel (xs.h) when H and I are
-//                   multiples of 256 and the group size a power of two, else on
-//                   k_gate_up / k_down below.
+//                   multiples of 256 and the group size a power of two (GGUF experts:
+//                   always); otherwise MLX experts run k_gate_up / k_down below, which
+//                   keep h in fp16.
 //   5. k_combine    y[t] = sum_s w[t,s] * partial[inv[t,s]] in slot order
 //                   (reference role: moe.py:479-501, fixed-order combine)
 // Each expert's weights are read once per column tile of its routed tokens.
@@ -41,7 +44,7 @@ MoeLayout moe_layout(int64_t T, int E, int top_k, int64_t H, int64_t I) {
   L.inv = o; o = align256(o + 4 * (size_t)L.R);
   L.tiles = o; o = align256(o + 4 * kTileInts * (size_t)L.max_tiles);
   L.ntiles = o; o = align256(o + 4);
-  L.h = o; o = align256(o + 2 * (size_t)L.R * (size_t)I);
+  L.h = o; o = align256(o + 4 * (size_t)L.R * (size_t)I);
   L.part = o; o = align256(o + 4 * (size_t)L.R * (size_t)H);
   L.total = o;
   return L;
@@ -400,7 +403,7 @@ __global__ __launch_bounds__(256) void k_combine(const float* part, const int32_
 // size a power of two); hipErrorNotSupported otherwise, before anything is launched.
 template <int GSH>
 static hipError_t experts_xs(const MoeArgs& m, const MoeLayout& L, const int32_t* sorted,
-                             const int32_t* tiles, const int32_t* ntiles, f16* h, float* part,
+                             const int32_t* tiles, const int32_t* ntiles, float* h, float* part,
                              hipStream_t st) {
   XsJob g{};
   g.a = m.gu;
@@ -417,7 +420,7 @@ static hipError_t experts_xs(const MoeArgs& m, const MoeLayout& L, const int32_t
   d.a = m.dn;
   d.sb = (uint32_t)(m.I / m.dn.gs * 2);
   d.x = h;
-  d.xbytes = (uint32_t)(L.R * m.I * 2);
+  d.xbytes = (uint32_t)(L.R * m.I * 4);
   d.xld = (int)m.I;
   d.N = (int)m.H;
   d.part = part;
@@ -429,11 +432,11 @@ static hipError_t experts_xs(const MoeArgs& m, const MoeLayout& L, const int32_t
 }
 
 static hipError_t launch_experts_xs(const MoeArgs& m, const MoeLayout& L, const int32_t* sorted,
-                                    const int32_t* tiles, const int32_t* ntiles, f16* h, float* part,
+                                    const int32_t* tiles, const int32_t* ntiles, float* h, float* part,
                                     hipStream_t st) {
   const int gs = m.gu.gs;
   if (m.H % 256 || m.I % 256 || m.H > 4096 || m.I > 8192 || (gs & (gs - 1)) || gs < 32 || gs > 4096 ||
-      L.max_tiles > 65535 || (uint64_t)m.T * m.H * 2 >= (1ull << 31) || (uint64_t)L.R * m.I * 2 >= (1ull << 31) ||
+      L.max_tiles > 65535 || (uint64_t)m.T * m.H * 2 >= (1ull << 31) || (uint64_t)L.R * m.I * 4 >= (1ull << 31) ||
       (uint64_t)(2 * m.I + 16) * m.gu.rb >= (1ull << 31) || (uint64_t)(m.H + 16) * m.dn.rb >= (1ull << 31))
     return hipErrorNotSupported;
   switch (gs) {
@@ -448,15 +451,14 @@ static hipError_t launch_experts_xs(const MoeArgs& m, const MoeLayout& L, const 
   }
 }
 
-hipError_t launch_mlx_moe(const MoeArgs& m, const MoeLayout& L, hipStream_t st) {
+// Router + sort (one fused workgroup for small batches) into the workspace.
+static hipError_t route_and_sort(const MoeArgs& m, const MoeLayout& L, hipStream_t st) {
   int32_t* idx = (int32_t*)(m.ws + L.idx);
   float* wts = (float*)(m.ws + L.wts);
   int32_t* sorted = (int32_t*)(m.ws + L.sorted);
   int32_t* inv = (int32_t*)(m.ws + L.inv);
   int32_t* tiles = (int32_t*)(m.ws + L.tiles);
   int32_t* ntiles = (int32_t*)(m.ws + L.ntiles);
-  f16* h = (f16*)(m.ws + L.h);
-  float* part = (float*)(m.ws + L.part);
   hipError_t e = hipSuccess;
   const size_t sort_lds = (size_t)(kSortWaves * m.E + 2 * m.E + 64) * sizeof(int);
   if (m.T <= kFusedTokens) {
@@ -471,34 +473,84 @@ hipError_t launch_mlx_moe(const MoeArgs& m, const MoeLayout& L, hipStream_t st) 
       return hipGetLastError();
     };
     const int vpl = (m.E + 63) / 64;
-    e = vpl <= 2 ? fused(k_route_sort<2>) : vpl <= 4 ? fused(k_route_sort<4>)
-      : vpl <= 8 ? fused(k_route_sort<8>) : fused(k_route_sort<16>);
-    if (e != hipSuccess) return e;
-  } else {
-    e = launch_router(m.logits, idx, wts, m.T, m.E, m.top_k, st);
-    if (e != hipSuccess) return e;
-    if (sort_lds > 65536) {
-      e = hipFuncSetAttribute((const void*)k_sort, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sort_lds);
-      if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL(k_sort, dim3(1), dim3(1024), sort_lds, st, idx, (int)L.R, m.E, m.top_k, sorted, inv, tiles,
-                       ntiles);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    return vpl <= 2 ? fused(k_route_sort<2>) : vpl <= 4 ? fused(k_route_sort<4>)
+         : vpl <= 8 ? fused(k_route_sort<8>) : fused(k_route_sort<16>);
   }
-  e = launch_experts_xs(m, L, sorted, tiles, ntiles, h, part, st);
+  e = launch_router(m.logits, idx, wts, m.T, m.E, m.top_k, st);
+  if (e != hipSuccess) return e;
+  if (sort_lds > 65536) {
+    e = hipFuncSetAttribute((const void*)k_sort, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sort_lds);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(k_sort, dim3(1), dim3(1024), sort_lds, st, idx, (int)L.R, m.E, m.top_k, sorted, inv, tiles,
+                     ntiles);
+  return hipGetLastError();
+}
+
+static hipError_t combine(const MoeArgs& m, const MoeLayout& L, hipStream_t st) {
+  hipLaunchKernelGGL(k_combine, dim3((unsigned)m.T, (unsigned)((m.H + 255) / 256)), dim3(256), 0, st,
+                     (const float*)(m.ws + L.part), (const int32_t*)(m.ws + L.inv), (const float*)(m.ws + L.wts),
+                     m.y, m.top_k, (int)m.H);
+  return hipGetLastError();
+}
+
+hipError_t launch_mlx_moe(const MoeArgs& m, const MoeLayout& L, hipStream_t st) {
+  int32_t* sorted = (int32_t*)(m.ws + L.sorted);
+  int32_t* tiles = (int32_t*)(m.ws + L.tiles);
+  int32_t* ntiles = (int32_t*)(m.ws + L.ntiles);
+  float* part = (float*)(m.ws + L.part);
+  hipError_t e = route_and_sort(m, L, st);
+  if (e != hipSuccess) return e;
+  e = launch_experts_xs(m, L, sorted, tiles, ntiles, (float*)(m.ws + L.h), part, st);
   if (e == hipErrorNotSupported) {
     (void)hipGetLastError();
+    f16* h16 = (f16*)(m.ws + L.h);             // this pair keeps h in fp16
     hipLaunchKernelGGL(k_gate_up, dim3((unsigned)L.max_tiles, (unsigned)((m.I + 15) / 16)), dim3(256), 0, st,
-                       m.gu, m.x, sorted, tiles, ntiles, h, m.top_k, (int)m.I);
+                       m.gu, m.x, sorted, tiles, ntiles, h16, m.top_k, (int)m.I);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(k_down, dim3((unsigned)L.max_tiles, (unsigned)((m.H + 15) / 16)), dim3(256), 0, st,
-                       m.dn, h, tiles, ntiles, part, (int)m.H);
+                       m.dn, h16, tiles, ntiles, part, (int)m.H);
     e = hipGetLastError();
   }
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_combine, dim3((unsigned)m.T, (unsigned)((m.H + 255) / 256)), dim3(256), 0, st,
-                     part, inv, wts, m.y, m.top_k, (int)m.H);
-  return hipGetLastError();
+  return combine(m, L, st);
+}
+
+bool gguf_moe_supported(int64_t T, int64_t H, int64_t I, const MoeLayout& L) {
+  // gate/up: two Q4_K matrices of K = H on 8-slot waves (H <= 4096); down: Q6_K of
+  // K = I on 8-slot waves (I <= 4096); 32-bit offsets within one expert and in the
+  // activation / h buffers
+  return H % 256 == 0 && I % 256 == 0 && H <= 4096 && I <= 4096 && L.max_tiles <= 65535 &&
+         (uint64_t)T * H * 2 < (1ull << 31) && (uint64_t)L.R * I * 4 < (1ull << 31) &&
+         (uint64_t)(2 * I + 16) * (H / 256 * 144) < (1ull << 31) && (uint64_t)(H + 16) * (I / 256 * 210) < (1ull << 31);
+}
+
+hipError_t launch_gguf_moe(const MoeArgs& m, const MoeLayout& L, hipStream_t st) {
+  if (!gguf_moe_supported(m.T, m.H, m.I, L)) return hipErrorNotSupported;
+  hipError_t e = route_and_sort(m, L, st);
+  if (e != hipSuccess) return e;
+  XsJob g{};
+  g.a = m.gu;
+  g.x = m.x;
+  g.xbytes = (uint32_t)(m.T * m.H * 2);
+  g.xld = (int)m.H;
+  g.M = (int)(m.T < 16 ? m.T : 16);
+  g.N = (int)m.I;
+  g.tiles = (const int32_t*)(m.ws + L.tiles);
+  g.ntiles = (const int32_t*)(m.ws + L.ntiles);
+  g.h = (float*)(m.ws + L.h);
+  XsJob d = g;
+  d.a = m.dn;
+  d.x = g.h;
+  d.xbytes = (uint32_t)(L.R * m.I * 4);
+  d.xld = (int)m.I;
+  d.N = (int)m.H;
+  d.part = (float*)(m.ws + L.part);
+  e = launch_xs<XsQ4K, 1>(g, L.max_tiles, 0, 0, st);
+  if (e != hipSuccess) return e == hipErrorNotSupported ? hipErrorInvalidValue : e;
+  e = launch_xs<XsQ6K, 2>(d, L.max_tiles, 0, 0, st);
+  if (e != hipSuccess) return e == hipErrorNotSupported ? hipErrorInvalidValue : e;
+  return combine(m, L, st);
 }
 
 }  // namespace alloy

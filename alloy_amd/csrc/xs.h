@@ -2,18 +2,18 @@
 // routed-expert MoE GEMVs), gfx950.
 //
 // Each wave owns a fixed range of K and keeps the activations of that range (16
-// token rows, zero past the row count) as v_mfma_f32_16x16x32_f16 A operands in
-// registers for the whole kernel; the workgroup's W waves cover all of K for the same
-// 16-row weight tiles and are reduced through LDS in a fixed order.  B = 16 weight
-// rows x one 32-element sub-block with the quants as exact fp16 integers (1024 + q,
-// or 1024 + 16q for a high nibble), so every product is exact; D (lane: weight row
-// l%16, tokens 4(l/16)+t) is fresh per sub-block and folded in fp32 as
+// token rows, zero past the row count) as MFMA A operands in registers for the whole
+// kernel; the workgroup's W waves cover all of K for the same 16-row weight tiles and
+// are reduced through LDS in a fixed order.  B = 16 weight rows with the quants as
+// exact fp16 integers (1024 + q, or 1024 + 16q for a high nibble), so every product
+// is exact.  The MFMAs of one scale group ("chain") accumulate D (lane: weight row
+// l%16, tokens 4(l/16)+t), which is folded in fp32 as
 //     y += s*D + c*X,
-// with the sub-block's scale s, offset c (the format's offset minus 1024 s) and X
-// the sub-block's activation sum per token, computed once per wave (ones operand)
-// into LDS.  Every weight byte of a group of tiles is requested before any is used.
+// with the group's scale s, offset c (the format's offset minus 1024 s) and X the
+// group's activation sum per token, computed once per wave (ones operand) into LDS.
+// Every weight byte of a group of tiles is requested before any is used.
 //
-// Units: 256 elements of a row (8 sub-blocks); a wave owns NS/8 units.
+// Units: 256 elements of a row; a wave owns NS/8 units (8 activation slots each).
 #pragma once
 #include <atomic>
 #include <type_traits>
@@ -24,21 +24,62 @@ namespace alloy {
 constexpr uint32_t kXsMagic = 0x64006400u;     // fp16 1024.0 in both halves
 
 // ---------------------------------------------------------------- format providers
-// load(): the lane's bytes of one unit of its row (kq = lane/16 selects the 8
-// elements of every sub-block that the lane feeds to the MFMA); bq<J>(): MFMA J's B
-// operand; sc<J>(): its scale and offset; xel(J, kq): the element offset in the unit
-// of the lane's 8 activations for MFMA J.  CHAIN: consecutive MFMAs that share one
-// scale and offset (their products are summed in the MFMA accumulator and folded
-// once).  PERM: the x element order that matches the unpack: 4 -> (0,2,1,3) per 4
-// elements, 8 -> (0,4,1,5,2,6,3,7).  rw / rs: byte offsets of the row in the weight
-// / scale buffers.
+// A provider describes one quantized format to the kernel:
+//   Raw, load(src, rw, rs, unit, kq, raw): the lane's bytes of one unit of its row
+//       (rw / rs: byte offsets of the row in the weight / scale buffers; kq = lane/16)
+//   xload(xr, off, S, kq): the lane's 8 activations for slot S (0..7) of a unit whose
+//       first element is at byte `off` of the activation buffer, in the order the
+//       unpack produces (A operands); xload32: the same 8 from an fp32 buffer
+//   NCH, chain<C>(xu, raw): chain C of the unit: its MFMAs on the unit's activation
+//       slots xu[0..7], summed in one accumulator D (all products exact)
+//   xsum<C>(xu): the same MFMAs against ones (the per-token activation sums X)
+//   sc<C>(raw, s, c): the chain's scale and offset: the chain contributes s D + c X.
+//   WIDE: whether 16 activation slots per wave (K up to 8192) or two tiles per
+//       reduction fit the registers.
 
-// Q4_K: unit = one 144-byte super-block; the lane reads the 16-byte header and bytes
-// 8kq .. 8kq+7 of each 32-byte quant pair (low nibbles: sub-block 2p, high: 2p+1).
+// 8 fp16 activations at byte `off` in the order (0,2,1,3, 4,6,5,7)
+__device__ __forceinline__ f16x8 xs_x8_perm4(__amdgpu_buffer_rsrc_t xr, uint32_t off) {
+  const u32x4 v = bld16(xr, off);
+  return __builtin_bit_cast(f16x8, u32x4{__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.y, v.x, 0x07060302u),
+                                         __builtin_amdgcn_perm(v.w, v.z, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u)});
+}
+// 8 fp16 activations at byte `off` in the order (0,4,1,5,2,6,3,7)
+__device__ __forceinline__ f16x8 xs_x8_perm8(__amdgpu_buffer_rsrc_t xr, uint32_t off) {
+  const u32x4 v = bld16(xr, off);
+  return __builtin_bit_cast(f16x8, u32x4{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                                         __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)});
+}
+// The four words of a as floats.  Each element is copied to a scalar before the
+// bit cast: a bit cast of a vector element expression itself has produced element 0.
+__device__ __forceinline__ void xs_u4_to_f(u32x4 a, float* f) {
+  const uint32_t t0 = a.x, t1 = a.y, t2 = a.z, t3 = a.w;
+  f[0] = __builtin_bit_cast(float, t0);
+  f[1] = __builtin_bit_cast(float, t1);
+  f[2] = __builtin_bit_cast(float, t2);
+  f[3] = __builtin_bit_cast(float, t3);
+}
+
+// 8 consecutive fp32 activations at byte `off`, reordered by ORD (index of the source
+// element for each position)
+template <int O0, int O1, int O2, int O3, int O4, int O5, int O6, int O7>
+__device__ __forceinline__ void xs_x8_f32(__amdgpu_buffer_rsrc_t xr, uint32_t off, float (&v)[8]) {
+  float f[8];
+  xs_u4_to_f(bld16(xr, off), f);
+  xs_u4_to_f(bld16(xr, off + 16u), f + 4);
+  v[0] = f[O0]; v[1] = f[O1]; v[2] = f[O2]; v[3] = f[O3]; v[4] = f[O4]; v[5] = f[O5]; v[6] = f[O6]; v[7] = f[O7];
+}
+__device__ __forceinline__ f32x4 xs_mfma32(f16x8 a, u32x4 b, f32x4 d) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, b), d, 0, 0, 0);
+}
+constexpr f16x8 kXsOnes = {1, 1, 1, 1, 1, 1, 1, 1};
+
+// Q4_K: unit = one 144-byte super-block; one chain per 32-element sub-block J (one
+// 16x16x32 MFMA).  The lane reads the 16-byte header and bytes 8kq .. 8kq+7 of each
+// 32-byte quant pair p (low nibbles: sub-block 2p, high: 2p+1, as 1024 + 16q).
 struct XsQ4K {
-  static constexpr int PERM = 4;
+  static constexpr int NCH = 8;
+  static constexpr bool WIDE = true;             // 16 slots per wave and 2 tiles fit
   struct Raw { u32x4 hd; uint2 q[4]; };
-  __device__ static int xel(int J, int kq) { return 32 * J + 8 * kq; }
   __device__ static void load(const Src& src, uint32_t rw, uint32_t, int unit, int kq, Raw& r) {
     const uint32_t bo = rw + (uint32_t)unit * 144u;
     r.hd = bld16(src.w, bo);
@@ -46,19 +87,29 @@ struct XsQ4K {
     for (int p = 0; p < 4; ++p)
       r.q[p] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(src.w, bo + 16u + 32u * p + 8u * kq, 0, 0));
   }
-  static constexpr int CHAIN = 1;
-  template <int J>
-  __device__ static u32x4 bq(const Raw& r) {
-    constexpr int p = J >> 1;
-    constexpr uint32_t m = (J & 1) ? 0x00F000F0u : 0x000F000Fu;
-    const uint32_t w0 = r.q[p].x, w1 = r.q[p].y;
-    return u32x4{(w0 & m) | kXsMagic, ((w0 >> 8) & m) | kXsMagic, (w1 & m) | kXsMagic, ((w1 >> 8) & m) | kXsMagic};
+  __device__ static f16x8 xload(__amdgpu_buffer_rsrc_t xr, uint32_t off, int S, int kq) {
+    return xs_x8_perm4(xr, off + 2u * (uint32_t)(32 * S + 8 * kq));
   }
-  template <int J>
+  __device__ static void xload32(__amdgpu_buffer_rsrc_t xr, uint32_t off, int S, int kq, float (&v)[8]) {
+    xs_x8_f32<0, 2, 1, 3, 4, 6, 5, 7>(xr, off + 4u * (uint32_t)(32 * S + 8 * kq), v);
+  }
+  template <int C>
+  __device__ static f32x4 chain(const f16x8* xu, const Raw& r) {
+    constexpr int p = C >> 1;
+    constexpr uint32_t m = (C & 1) ? 0x00F000F0u : 0x000F000Fu;
+    const uint32_t w0 = r.q[p].x, w1 = r.q[p].y;
+    const u32x4 b = {(w0 & m) | kXsMagic, ((w0 >> 8) & m) | kXsMagic, (w1 & m) | kXsMagic, ((w1 >> 8) & m) | kXsMagic};
+    return xs_mfma32(xu[C], b, f32x4{0.f, 0.f, 0.f, 0.f});
+  }
+  template <int C>
+  __device__ static f32x4 xsum(const f16x8* xu) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(xu[C], kXsOnes, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+  }
+  template <int C>
   __device__ static void sc(const Raw& r, float& s, float& c) {
     uint32_t scl, mn;
-    q4k_scale_min(r.hd.y, r.hd.z, r.hd.w, J, scl, mn);
-    s = h2f(r.hd.x) * (float)scl * ((J & 1) ? 0.0625f : 1.f);
+    q4k_scale_min(r.hd.y, r.hd.z, r.hd.w, C, scl, mn);
+    s = h2f(r.hd.x) * (float)scl * ((C & 1) ? 0.0625f : 1.f);
     c = -(h2f(r.hd.x >> 16) * (float)mn) - 1024.f * s;
   }
 };
@@ -68,16 +119,17 @@ struct XsQ4K {
 // consecutive words per load (LW = 2^min(GSH, 2)); load l of lane kq covers words
 // 4 LW l + LW kq + h (h < LW), and MFMA J = LW l + h takes word slot h of load l, so
 // the four lanes of one MFMA read four words of one group (a group is 4 << GSH
-// words).  Scales and biases of the unit's groups: a row's groups are contiguous.
+// words).  One chain per group of the unit (its MFMAs share the scale and bias).
+// Scales and biases of the unit's groups: a row's groups are contiguous.
 template <int GSH>
 struct XsMLX {
-  static constexpr int PERM = 8;
   static constexpr int LW = GSH >= 2 ? 4 : 1 << GSH;    // words per lane load
   static constexpr int G = GSH >= 3 ? 1 : 8 >> GSH;     // groups per unit
   static constexpr int NW = G >= 2 ? G / 2 : 1;         // scale words per unit
+  static constexpr int CH = 8 / G;                      // MFMAs per chain
+  static constexpr int NCH = G;
+  static constexpr bool WIDE = true;
   struct Raw { uint32_t q[8]; uint32_t sc[NW], bi[NW]; };
-  // element offset within the unit of lane kq's 8 elements for MFMA J
-  __device__ static int xel(int J, int kq) { return 8 * (4 * LW * (J / LW) + LW * kq + J % LW); }
   __device__ static void load(const Src& src, uint32_t rw, uint32_t rs, int unit, int kq, Raw& r) {
     const uint32_t bo = rw + (uint32_t)unit * 128u + 4u * LW * kq;
 #pragma unroll
@@ -112,18 +164,106 @@ struct XsMLX {
       r.bi[0] = bld2(src.b, so);
     }
   }
-  static constexpr int CHAIN = GSH >= 3 ? 8 : 1 << GSH;   // MFMAs per group
-  template <int J>
-  __device__ static u32x4 bq(const Raw& r) {
-    const uint32_t w = r.q[J];
-    return u32x4{(w & 0x000F000Fu) | kXsMagic, ((w >> 4) & 0x000F000Fu) | kXsMagic,
-                 ((w >> 8) & 0x000F000Fu) | kXsMagic, ((w >> 12) & 0x000F000Fu) | kXsMagic};
+  // slot S = MFMA S: word 4 LW (S / LW) + LW kq + S % LW of the unit
+  __device__ static f16x8 xload(__amdgpu_buffer_rsrc_t xr, uint32_t off, int S, int kq) {
+    return xs_x8_perm8(xr, off + 16u * (uint32_t)(4 * LW * (S / LW) + LW * kq + S % LW));
   }
-  template <int J>
+  __device__ static void xload32(__amdgpu_buffer_rsrc_t xr, uint32_t off, int S, int kq, float (&v)[8]) {
+    xs_x8_f32<0, 4, 1, 5, 2, 6, 3, 7>(xr, off + 32u * (uint32_t)(4 * LW * (S / LW) + LW * kq + S % LW), v);
+  }
+  template <int C>
+  __device__ static f32x4 chain(const f16x8* xu, const Raw& r) {
+    f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const uint32_t w = r.q[C * CH + i];
+      const u32x4 b = {(w & 0x000F000Fu) | kXsMagic, ((w >> 4) & 0x000F000Fu) | kXsMagic,
+                       ((w >> 8) & 0x000F000Fu) | kXsMagic, ((w >> 12) & 0x000F000Fu) | kXsMagic};
+      d = xs_mfma32(xu[C * CH + i], b, d);
+    }
+    return d;
+  }
+  template <int C>
+  __device__ static f32x4 xsum(const f16x8* xu) {
+    f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < CH; ++i) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xu[C * CH + i], kXsOnes, d, 0, 0, 0);
+    return d;
+  }
+  template <int C>
   __device__ static void sc(const Raw& r, float& s, float& c) {
-    constexpr int g = GSH >= 3 ? 0 : (4 * LW * (J / LW)) / (4 << GSH);   // group within the unit
-    s = h2f(r.sc[g >> 1] >> (16 * (g & 1)));
-    c = h2f(r.bi[g >> 1] >> (16 * (g & 1))) - 1024.f * s;
+    s = h2f(r.sc[C >> 1] >> (16 * (C & 1)));
+    c = h2f(r.bi[C >> 1] >> (16 * (C & 1))) - 1024.f * s;
+  }
+};
+
+// Q6_K: unit = one 210-byte super-block (2-byte aligned in the row).  One chain per
+// 16-element scale group C (element 16 C + l, l < 16; group C = sub-block C / 2 of
+// 32, half C % 2), one 16x16x16 MFMA: lane kq supplies elements 16 C + 4 kq .. + 3,
+// as 1024 + (ql nibble | qh bits << 4) (the stored 6-bit value; q = that - 32).
+// Element e = 128 h + 32 s + l: ql byte 64 h + 32 (s & 1) + l, nibble 4 (s >> 1);
+// qh byte 128 + 32 h + l, bits 2 s; scale byte 192 + C (int8); d at byte 208.
+// The lane's ql dwords m = 4 h + 2 (s & 1) + (l >= 16) and qh dwords m' = 2 h + (l >= 16)
+// are read with 8-byte loads from the 4-byte aligned address below and realigned.
+struct XsQ6K {
+  static constexpr int NCH = 16;
+  static constexpr bool WIDE = false;            // (a 16-slot wave or 2 tiles would spill)
+  struct Raw { uint32_t ql[8], qh[4], scw[4], d; };
+  __device__ static uint32_t word_a2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const uint32_t sh = off & 2u;
+    const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off - sh, 0, 0));
+    return __builtin_amdgcn_alignbyte(v.y, v.x, sh);
+  }
+  __device__ static void load(const Src& src, uint32_t rw, uint32_t, int unit, int kq, Raw& r) {
+    const uint32_t bo = rw + (uint32_t)unit * 210u;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) r.ql[m] = word_a2(src.w, bo + 16u * m + 4u * kq);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) r.qh[m] = word_a2(src.w, bo + 128u + 16u * m + 4u * kq);
+    {
+      const uint32_t so = bo + 192u, sh = so & 2u, base = so - sh;
+      const u32x4 a = bld16(src.w, base);
+      const uint32_t e = bld4(src.w, base + 16u);
+      r.scw[0] = __builtin_amdgcn_alignbyte(a.y, a.x, sh);
+      r.scw[1] = __builtin_amdgcn_alignbyte(a.z, a.y, sh);
+      r.scw[2] = __builtin_amdgcn_alignbyte(a.w, a.z, sh);
+      r.scw[3] = __builtin_amdgcn_alignbyte(e, a.w, sh);
+    }
+    r.d = bld2(src.w, bo + 208u);
+  }
+  // slot S holds elements 32 S + 4 kq .. + 3 (low 4 halves) and 32 S + 16 + 4 kq .. + 3
+  __device__ static f16x8 xload(__amdgpu_buffer_rsrc_t xr, uint32_t off, int S, int kq) {
+    const uint32_t o = off + 2u * (uint32_t)(32 * S + 4 * kq);
+    const uint2 lo = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(xr, o, 0, 0));
+    const uint2 hi = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(xr, o + 32u, 0, 0));
+    return __builtin_bit_cast(f16x8, u32x4{lo.x, lo.y, hi.x, hi.y});
+  }
+  __device__ static void xload32(__amdgpu_buffer_rsrc_t xr, uint32_t off, int S, int kq, float (&v)[8]) {
+    const uint32_t o = off + 4u * (uint32_t)(32 * S + 4 * kq);
+    xs_u4_to_f(bld16(xr, o), v);
+    xs_u4_to_f(bld16(xr, o + 64u), v + 4);
+  }
+  __device__ static f16x4 half4(const f16x8& v, int hi) {
+    return hi ? __builtin_shufflevector(v, v, 4, 5, 6, 7) : __builtin_shufflevector(v, v, 0, 1, 2, 3);
+  }
+  template <int C>
+  __device__ static f32x4 chain(const f16x8* xu, const Raw& r) {
+    constexpr int S = C >> 1, g2 = C & 1, h = S >> 2, s = S & 3;
+    const uint32_t ql = r.ql[4 * h + 2 * (s & 1) + g2], qh = r.qh[2 * h + g2];
+    const uint32_t v = ((ql >> (4 * (s >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * s)) & 0x03030303u) << 4);
+    const uint2 b = {__builtin_amdgcn_perm(0u, v, 0x0c010c00u) | kXsMagic, __builtin_amdgcn_perm(0u, v, 0x0c030c02u) | kXsMagic};
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(half4(xu[S], g2), __builtin_bit_cast(f16x4, b),
+                                                  f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+  }
+  template <int C>
+  __device__ static f32x4 xsum(const f16x8* xu) {
+    const f16x4 ones = {1, 1, 1, 1};
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(half4(xu[C >> 1], C & 1), ones, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+  }
+  template <int C>
+  __device__ static void sc(const Raw& r, float& s, float& c) {
+    s = h2f(r.d) * (float)(int8_t)((r.scw[C >> 2] >> (8 * (C & 3))) & 0xFFu);
+    c = -1056.f * s;                              // (q - 32) with q stored as 1024 + q
   }
 };
 
@@ -131,12 +271,15 @@ struct XsMLX {
 // MODE 0: dense y[t, n] = x[t] . W[n] for t < M (x [M, xld] fp16, y fp16 or fp32).
 // MODE 1: routed gate/up.  Workgroup row y = column tile (expert e, sorted routes
 //         p0 .. p0+cnt); token slot t gathers x[token t of the record]; weight rows
-//         e*2N + n (gate) and e*2N + N + n (up); h[p0+t, n] = silu(gate) * up (fp16).
-// MODE 2: routed down: x = h[p0+t]; weight rows e*N + n; part[p0+t, n] (fp32).
+//         e*2N + n (gate) and e*2N + N + n (up); h[p0+t, n] = silu(gate) * up (fp32).
+// MODE 2: routed down: x = h[p0+t] (fp32); weight rows e*N + n; part[p0+t, n] (fp32).
+//         Each token's activations enter the MFMA as fp16 after a power-of-two
+//         scaling that puts the token's largest |h| in [2^14, 2^15) (fp16 range,
+//         11-bit precision whatever the magnitude); the result is scaled back.
 struct XsJob {
   QArgs a;                 // whole matrix (all experts for MODE 1/2)
   uint32_t sb;             // bytes per row of scales / biases (MLX), else 0
-  const f16* x;
+  const void* x;           // fp16 (MODE 0/1) or fp32 (MODE 2) activations
   uint32_t xbytes;         // bytes of x readable (bounds of the activation buffer)
   int xld;                 // elements per activation row
   int M;                   // MODE 0: activation rows; MODE 1/2: bound on routes per tile
@@ -145,7 +288,7 @@ struct XsJob {
   int y_f32;
   const int32_t* tiles;    // MODE 1/2: column tile records, kTileInts ints each
   const int32_t* ntiles;   // number of valid records
-  f16* h;                  // MODE 1 output, MODE 2 input
+  float* h;                // MODE 1 output
   float* part;             // MODE 2 output
   int W;                   // waves per workgroup (set by the launcher)
 };
@@ -166,12 +309,13 @@ __device__ __forceinline__ void xs_static_for(Fn&& f) {
 // tiles' weights are requested before the activations are waited for.  Rows past the
 // matrix, tiles past the end and activations past the buffers read as zero (buffer
 // bounds, no memory traffic); outputs past the valid rows and tokens are not
-// stored.  Dynamic LDS: Xs[W][NS][16] + red[W][RT][64][4 NM] floats.
+// stored.  Dynamic LDS: Xs[W][NS/8][NCH][16] + red[W][RT][64][4 NM] (+ tmx[W][16]
+// + tsc[16] for MODE 2) floats.
 template <class P, int MODE, int NS, int TT, int RT, bool PIPE, class YT>
 __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
   constexpr int NM = MODE == 1 ? 2 : 1;          // weight matrices per output
   constexpr int UPW = NS / 8;                    // units per wave
-  constexpr int CH = P::CHAIN, NSC = NS / CH;    // chains of sub-blocks per wave
+  constexpr int NCH = P::NCH;                    // chains per unit
   using Raw = typename P::Raw;
   extern __shared__ __attribute__((aligned(16))) float xs_smem[];
   const int K = j.a.K, KU = K >> 8;
@@ -179,8 +323,10 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
   // is read with a vector load, and one issued after the weight prefetch makes every
   // later wait drain the prefetch too
   const int W = j.W, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  float* Xs = xs_smem;                                   // [W][NSC][16]
-  float* red = xs_smem + W * NSC * 16;                   // [W][RT][64][4 NM]
+  float* Xs = xs_smem;                                   // [W][UPW][NCH][16]
+  float* red = xs_smem + W * UPW * NCH * 16;             // [W][RT][64][4 NM]
+  float* tmx = red + W * RT * 64 * 4 * NM;               // [W][16] token |x| maxima (MODE 2)
+  float* tsc = tmx + W * 16;                             // [16] token scales (MODE 2)
   const int n16 = lane & 15, kq = lane >> 4;
   const int u0 = wave * UPW;                             // first unit of this wave
   const int nu = KU - u0 < UPW ? KU - u0 : UPW;          // units present (uniform)
@@ -229,8 +375,9 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
     }
   };
 
-  // A operands: token slot n16, elements 256 u + xel(s % 8, kq) in PERM order
+  // A operands: token slot n16, slots 8 u .. 8 u + 7 of unit u0 + u (provider order)
   f16x8 xa[NS];
+  constexpr uint32_t XB = MODE == 2 ? 4u : 2u;           // bytes per activation
   auto load_x = [&]() {
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)j.x, (short)0, (int)j.xbytes, ALLOY_RSRC_DW3);
     uint32_t xrow = 0x80000000u;                         // past the buffer: zeros
@@ -238,25 +385,43 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
       int64_t r = n16;
       if constexpr (MODE == 1) r = tok;
       else if constexpr (MODE == 2) r = p0 + n16;
-      xrow = (uint32_t)(r * j.xld) * 2u;
+      xrow = (uint32_t)(r * j.xld) * XB;
     }
-    u32x4 v[NS];
+    if constexpr (MODE != 2) {
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const uint32_t off = (s >> 3) < nu ? xrow + 2u * (uint32_t)(256 * (u0 + (s >> 3)) + P::xel(s & 7, kq))
-                                         : 0x80000000u;
-      v[s] = bld16(xr, off);
-    }
+      for (int s = 0; s < NS; ++s) {
+        const uint32_t off = (s >> 3) < nu ? xrow + 512u * (uint32_t)(u0 + (s >> 3)) : 0x80000000u;
+        xa[s] = P::xload(xr, off, s & 7, kq);
+      }
+    } else {
+      float v[NS][8];
+      float m = 0.f;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      u32x4 pv;
-      if constexpr (P::PERM == 4)
-        pv = u32x4{__builtin_amdgcn_perm(v[s].y, v[s].x, 0x05040100u), __builtin_amdgcn_perm(v[s].y, v[s].x, 0x07060302u),
-                   __builtin_amdgcn_perm(v[s].w, v[s].z, 0x05040100u), __builtin_amdgcn_perm(v[s].w, v[s].z, 0x07060302u)};
-      else
-        pv = u32x4{__builtin_amdgcn_perm(v[s].z, v[s].x, 0x05040100u), __builtin_amdgcn_perm(v[s].z, v[s].x, 0x07060302u),
-                   __builtin_amdgcn_perm(v[s].w, v[s].y, 0x05040100u), __builtin_amdgcn_perm(v[s].w, v[s].y, 0x07060302u)};
-      xa[s] = __builtin_bit_cast(f16x8, pv);
+      for (int s = 0; s < NS; ++s) {
+        const uint32_t off = (s >> 3) < nu ? xrow + 1024u * (uint32_t)(u0 + (s >> 3)) : 0x80000000u;
+        P::xload32(xr, off, s & 7, kq, v[s]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[s][i]));
+      }
+      // the token's largest |h| over the workgroup (lanes n16 + 16 kq, then the waves)
+      m = fmaxf(m, __shfl_xor(m, 16, 64));
+      m = fmaxf(m, __shfl_xor(m, 32, 64));
+      if (kq == 0) tmx[wave * 16 + n16] = m;
+      __syncthreads();
+      float tm = 0.f;
+      for (int w = 0; w < W; ++w) tm = fmaxf(tm, tmx[w * 16 + n16]);
+      int ex = 0;
+      if (tm > 0.f && tm <= 3.0e38f) (void)frexpf(tm, &ex);     // tm = f 2^ex, f in [0.5, 1)
+      const int sh = tm > 0.f && tm <= 3.0e38f ? ex - 15 : 0;   // tm 2^-sh in [2^14, 2^15)
+      const float down = ldexpf(1.f, -sh);
+      if (wave == 0 && kq == 0) tsc[n16] = ldexpf(1.f, sh);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        f16x8 a;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a[i] = (f16)(v[s][i] * down);
+        xa[s] = a;
+      }
     }
   };
 
@@ -272,19 +437,14 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
 #pragma unroll
       for (int u = 0; u < UPW; ++u) {
         if (u >= nu) break;                      // uniform; keeps xa[] statically indexed
-        xs_static_for<0, 8 / CH>([&](auto cc) {
+        xs_static_for<0, NCH>([&](auto cc) {
           constexpr int C = decltype(cc)::value;
-          const f32x4 xsum = *(const f32x4*)&Xs[(wave * NSC + (8 / CH) * u + C) * 16 + 4 * kq];
+          const f32x4 xsum = *(const f32x4*)&Xs[((wave * UPW + u) * NCH + C) * 16 + 4 * kq];
 #pragma unroll
           for (int mi = 0; mi < NM; ++mi) {
-            f32x4 d = {0.f, 0.f, 0.f, 0.f};
-            xs_static_for<0, CH>([&](auto jc) {
-              constexpr int J = C * CH + decltype(jc)::value;
-              const u32x4 b = P::template bq<J>(raw[r][mi][u]);
-              d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[8 * u + J], __builtin_bit_cast(f16x8, b), d, 0, 0, 0);
-            });
+            const f32x4 d = P::template chain<C>(&xa[8 * u], raw[r][mi][u]);
             float sc, off;
-            P::template sc<C * CH>(raw[r][mi][u], sc, off);
+            P::template sc<C>(raw[r][mi][u], sc, off);
 #pragma unroll
             for (int tt = 0; tt < TTR; ++tt) {
               const float dv = d[tt];
@@ -312,9 +472,9 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
       if constexpr (MODE == 0) {
         ((YT*)j.y)[(int64_t)tk * j.N + n] = (YT)v0;
       } else if constexpr (MODE == 1) {
-        j.h[(int64_t)(p0 + tk) * j.N + n] = (f16)(v0 * __builtin_amdgcn_rcpf(1.f + __expf(-v0)) * v1);
+        j.h[(int64_t)(p0 + tk) * j.N + n] = v0 * __builtin_amdgcn_rcpf(1.f + __expf(-v0)) * v1;
       } else {
-        j.part[(int64_t)(p0 + tk) * j.N + n] = v0;
+        j.part[(int64_t)(p0 + tk) * j.N + n] = v0 * tsc[tk];
       }
     }
     __syncthreads();
@@ -324,16 +484,14 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
   int t = blockIdx.x * RT;
   load_x();                                      // x first: its sums overlap the weight loads
   load_tiles(ra, t);
-  {
-    // X per chain of sub-blocks: tokens 4kq .. 4kq+3 in lane 16 kq
-    const f16x8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+  // X per chain: tokens 4kq .. 4kq+3 in lane 16 kq
 #pragma unroll
-    for (int c = 0; c < NSC; ++c) {
-      f32x4 X = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int i = 0; i < CH; ++i) X = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[c * CH + i], ones, X, 0, 0, 0);
-      if (n16 == 0) *(f32x4*)&Xs[(wave * NSC + c) * 16 + 4 * kq] = X;
-    }
+  for (int u = 0; u < UPW; ++u) {
+    xs_static_for<0, NCH>([&](auto cc) {
+      constexpr int C = decltype(cc)::value;
+      const f32x4 X = P::template xsum<C>(&xa[8 * u]);
+      if (n16 == 0) *(f32x4*)&Xs[((wave * UPW + u) * NCH + C) * 16 + 4 * kq] = X;
+    });
   }
   __syncthreads();
   auto run = [&](auto ttc) {
@@ -402,15 +560,16 @@ hipError_t launch_xs(const XsJob& j, int64_t tiles_y, int64_t cap, int rt, hipSt
     return hipErrorNotSupported;
   const int KS = K / 32;
   const int ns = KS <= 8 * 16 ? 8 : KS <= 16 * 16 ? 16 : 0;   // at most 16 waves
-  if (!ns || (MODE == 1 && ns == 16)) return hipErrorNotSupported;   // (two matrices: 8 sub-blocks)
+  if (!ns || ((MODE == 1 || !P::WIDE) && ns == 16)) return hipErrorNotSupported;   // (registers)
   if (MODE != 0 && tiles_y > 65535) return hipErrorNotSupported;
   if (MODE != 0 && tiles_y <= 0) return hipSuccess;
   const int W = (KS + ns - 1) / ns;
   const int64_t tiles = (j.N + 15) / 16;
   // 16 sub-blocks per wave leave registers for one tile in flight only
-  rt = (ns == 16 || MODE != 0 || rt < 2) ? 1 : 2;
+  rt = (ns == 16 || MODE != 0 || rt < 2 || !P::WIDE) ? 1 : 2;
   const int64_t groups = (tiles + rt - 1) / rt;
-  const size_t lds = (size_t)W * (ns / P::CHAIN) * 16 * 4 + (size_t)W * rt * 64 * 4 * NM * 4;
+  const size_t lds = (size_t)W * (ns / 8) * P::NCH * 16 * 4 + (size_t)W * rt * 64 * 4 * NM * 4 +
+                     (MODE == 2 ? (size_t)(W * 16 + 16) * 4 : 0);
   // token slots per lane: a tile holds at most min(M, 16) rows (routed tiles: one
   // route per token and expert, so at most min(T, 16) with j.M = T)
   const int tt = j.M <= 1 ? 1 : j.M == 2 ? 2 : 4;
@@ -443,8 +602,10 @@ hipError_t launch_xs(const XsJob& j, int64_t tiles_y, int64_t cap, int rt, hipSt
     auto pick = [&](auto ttc, auto yt) -> hipError_t {
       constexpr int TT = decltype(ttc)::value;
       using YT = decltype(yt);
-      if (ns == 16) return go(k_gemv_xs<P, 0, 16, TT, 1, false, YT>, false);
-      if (rt == 2) return go(k_gemv_xs<P, 0, 8, TT, 2, true, YT>, true);
+      if constexpr (P::WIDE) {
+        if (ns == 16) return go(k_gemv_xs<P, 0, 16, TT, 1, false, YT>, false);
+        if (rt == 2) return go(k_gemv_xs<P, 0, 8, TT, 2, true, YT>, true);
+      }
       if (many(k_gemv_xs<P, 0, 8, TT, 1, false, YT>)) return go(k_gemv_xs<P, 0, 8, TT, 1, true, YT>, true);
       return go(k_gemv_xs<P, 0, 8, TT, 1, false, YT>, false);
     };
@@ -453,7 +614,7 @@ hipError_t launch_xs(const XsJob& j, int64_t tiles_y, int64_t cap, int rt, hipSt
   } else {
     auto pick = [&](auto ttc) -> hipError_t {
       constexpr int TT = decltype(ttc)::value;
-      if constexpr (MODE == 2) {
+      if constexpr (MODE == 2 && P::WIDE) {
         if (ns == 16) return go(k_gemv_xs<P, 2, 16, TT, 1, false, float>, false);
       }
       // enough workgroups to fill the chip; beyond that, loop over output tiles (the

@@ -125,3 +125,62 @@ class MLXMoeExperts(torch.nn.Module):
             flat, logits, self.gate_up_qweight, self.gate_up_scales, self.gate_up_biases, self.down_qweight,
             self.down_scales, self.down_biases, self.num_experts, self.top_k, self.moe_intermediate)
         return y.reshape(*shape[:-1], self.hidden_size)
+
+
+class GGUFQwen35MoeExperts(torch.nn.Module):
+    """Stacked GGUF routed experts (``S/models/qwen3_5.py:232-301``): ``gate_up_blocks``
+    (E, 2I, (H/256)*144) native Q4_K with rows ``[0:I]`` gate and ``[I:2I]`` up, and
+    ``down_qweight`` (E, H, (I/256)*210) Q6_K.  A weight holder: the compute runs in
+    ``gguf_moe_routed``, driven by :class:`GGUFQwen35MoeBlock`; ``forward`` raises."""
+
+    def __init__(self, *, gate_up_blocks: torch.Tensor, down_qweight: torch.Tensor, num_experts: int,
+                 hidden_size: int, moe_intermediate_size: int) -> None:
+        super().__init__()
+        if hidden_size % 256 != 0 or moe_intermediate_size % 256 != 0:
+            raise ValueError("Qwen3.5-MoE expert dims must be divisible by 256: "
+                             f"hidden={hidden_size} moe_intermediate={moe_intermediate_size}")
+        expected = {"gate_up_blocks": (num_experts, 2 * moe_intermediate_size, hidden_size // 256 * 144),
+                    "down_qweight": (num_experts, hidden_size, moe_intermediate_size // 256 * 210)}
+        actual = {"gate_up_blocks": tuple(gate_up_blocks.shape), "down_qweight": tuple(down_qweight.shape)}
+        if actual != expected:
+            raise ValueError(f"Qwen3.5-MoE expert weight shapes do not match config: got {actual} expected {expected}")
+        if gate_up_blocks.dtype is not torch.uint8 or down_qweight.dtype is not torch.uint8:
+            raise TypeError("Qwen3.5-MoE expert weights must be uint8 packed blocks")
+        self.num_experts = int(num_experts)
+        self.hidden_size = int(hidden_size)
+        self.moe_intermediate_size = int(moe_intermediate_size)
+        self.register_buffer("gate_up_blocks", gate_up_blocks.contiguous())
+        self.register_buffer("down_qweight", down_qweight.contiguous())
+
+    def forward(self, *args, **kwargs):
+        raise RuntimeError("GGUFQwen35MoeExperts is a weight holder; compute is driven by GGUFQwen35MoeBlock "
+                           "via the gguf_moe_routed op, not this forward.")
+
+
+class GGUFQwen35MoeBlock(torch.nn.Module):
+    """Sparse MoE block (``S/models/qwen3_5.py:304-343``):
+    ``out = gguf_moe_routed(x, x @ Wr^T, experts...) + sigmoid(Wg x) * shared(x)``.
+
+    ``orig_block`` provides ``gate`` (router linear), ``experts``
+    (:class:`GGUFQwen35MoeExperts`), ``shared_expert`` and ``shared_expert_gate``."""
+
+    def __init__(self, orig_block: torch.nn.Module, *, num_experts: int, top_k: int, moe_intermediate: int) -> None:
+        super().__init__()
+        self.gate = orig_block.gate
+        self.experts = orig_block.experts
+        self.shared_expert = orig_block.shared_expert
+        self.shared_expert_gate = orig_block.shared_expert_gate
+        self.num_experts = int(num_experts)
+        self.top_k = int(top_k)
+        self.moe_intermediate = int(moe_intermediate)
+
+    def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        in_shape = hidden_states.shape
+        x = hidden_states.reshape(-1, in_shape[-1])
+        router_logits = torch.nn.functional.linear(x, self.gate.weight)
+        routed = torch.ops.alloy.gguf_moe_routed(x, router_logits, self.experts.gate_up_blocks,
+                                                 self.experts.down_qweight, self.num_experts, self.top_k,
+                                                 self.moe_intermediate)
+        shared = self.shared_expert(x)
+        shared = torch.sigmoid(self.shared_expert_gate(x)) * shared
+        return (routed + shared).reshape(in_shape)

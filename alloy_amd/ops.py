@@ -187,6 +187,46 @@ def mlx_moe_routed(hidden, router_logits, gate_up_qweight, gate_up_scales, gate_
     return y
 
 
+def gguf_moe_routed(hidden, router_logits, gate_up_blocks, down_qweight, num_experts: int, top_k: int,
+                    moe_intermediate: int, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Routed GGUF experts (Q4_K fused gate/up, Q6_K down) -> float32 (T, H), like the
+    reference's ``gguf_moe_routed`` (``custom_ops.py:59-66``, ``ops/moe.py:110-249``)."""
+    T, H, I, E = shape_gguf_moe(hidden, router_logits, gate_up_blocks, down_qweight, num_experts, top_k,
+                                moe_intermediate)
+    dev = _same_device(hidden, router_logits, gate_up_blocks, down_qweight)
+    hidden = hidden.contiguous()
+    logits = router_logits.to(torch.float32).contiguous()
+    need = moe_workspace_bytes(T, E, top_k, H, I)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+    y = torch.empty((T, H), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call("alloy_gguf_moe_routed", _p(hidden), _p(logits), _p(gate_up_blocks.contiguous()),
+                  _p(down_qweight.contiguous()), E, top_k, T, H, I, _p(workspace), workspace.numel(), _p(y),
+                  _stream(dev))
+    return y
+
+
+def shape_gguf_moe(hidden, router_logits, gate_up_blocks, down_qweight, num_experts, top_k, moe_intermediate):
+    if hidden.ndim != 2 or hidden.dtype != torch.float16:
+        raise TypeError("hidden must be float16 (T, H)")
+    T, H = hidden.shape
+    E, I = int(num_experts), int(moe_intermediate)
+    if H % 256 or I % 256:
+        raise ValueError(f"expert dims must be divisible by 256: hidden={H} moe_intermediate={I}")
+    if not router_logits.dtype.is_floating_point or tuple(router_logits.shape) != (T, E):
+        raise ValueError(f"router_logits must be floating point {(T, E)}")
+    expected = {"gate_up_blocks": (E, 2 * I, H // 256 * 144), "down_qweight": (E, H, I // 256 * 210)}
+    actual = {"gate_up_blocks": tuple(gate_up_blocks.shape), "down_qweight": tuple(down_qweight.shape)}
+    if actual != expected:
+        raise ValueError(f"expert weight shapes do not match: got {actual} expected {expected}")
+    if gate_up_blocks.dtype != torch.uint8 or down_qweight.dtype != torch.uint8:
+        raise TypeError("expert weights must be uint8 packed blocks")
+    if not (0 < top_k <= E):
+        raise ValueError(f"top_k={top_k} invalid for {E} experts")
+    return T, H, I, E
+
+
 def shape_moe(hidden, router_logits, gu_q, gu_s, gu_b, dn_q, dn_s, dn_b, num_experts, top_k, moe_intermediate):
     if hidden.ndim != 2 or hidden.dtype != torch.float16:
         raise TypeError("hidden must be float16 (T, H)")
@@ -227,6 +267,11 @@ _LIB.define("batched_mlx_q4_mm(Tensor activations, Tensor[] qweights, Tensor[] s
 # wire-block Q8_0 / Q5_0 (the raw GGUF blob; the reference only has the split ops)
 _LIB.define("gguf_q8_0_blocks_mm(Tensor activations, Tensor blocks) -> Tensor")
 _LIB.define("gguf_q5_0_blocks_mm(Tensor activations, Tensor blocks) -> Tensor")
+# GGUF routed experts (reference custom_ops.py:59-66)
+_LIB.define(
+    "gguf_moe_routed(Tensor hidden, Tensor router_logits, Tensor gate_up_blocks, "
+    "Tensor down_qweight, int num_experts, int top_k, int moe_intermediate) -> Tensor"
+)
 # MLX-4 routed experts (the MLX counterpart of the reference's gguf_moe_routed)
 _LIB.define(
     "mlx_moe_routed(Tensor hidden, Tensor router_logits, Tensor gate_up_qweight, Tensor gate_up_scales, "
@@ -340,6 +385,13 @@ for _name, _single in _BATCHED.items():
 
 
 torch.library.impl(_LIB, "mlx_moe_routed", "CUDA")(mlx_moe_routed)
+torch.library.impl(_LIB, "gguf_moe_routed", "CUDA")(gguf_moe_routed)
+
+
+@torch.library.impl(_LIB, "gguf_moe_routed", "Meta")
+def _gguf_moe_meta(hidden, router_logits, gate_up_blocks, down_qweight, num_experts, top_k, moe_intermediate):
+    shape_gguf_moe(hidden, router_logits, gate_up_blocks, down_qweight, num_experts, top_k, moe_intermediate)
+    return torch.empty((hidden.shape[0], hidden.shape[1]), dtype=torch.float32, device=hidden.device)
 
 
 @torch.library.impl(_LIB, "mlx_moe_routed", "Meta")

@@ -167,6 +167,22 @@ alloy_status alloy_mlx_moe_routed(const void* hidden, const float* router_logits
                                   int64_t H, int64_t I, void* workspace, size_t workspace_bytes,
                                   float* y, void* stream);
 
+/*
+ * Routed-expert MoE block over GGUF experts — torch.ops.alloy.gguf_moe_routed
+ * (custom_ops.py:59-66; handler packages/alloy-torch/src/alloy_torch/ops/moe.py:110-249;
+ * containers packages/alloy-server/src/alloy_server/models/qwen3_5.py:232-343):
+ *   same routing and composition as alloy_mlx_moe_routed, with
+ *   gate_up_blocks u8[E, 2I, (H/256)*144] native Q4_K (rows [0:I] gate, [I:2I] up),
+ *   down_qweight   u8[E, H, (I/256)*210] Q6_K.
+ *   hidden f16[T,H]; router_logits f32[T,E]; y f32[T,H].  H and I multiples of 256
+ *   (ALLOY_E_SHAPE otherwise, as the reference's containers require), at most 4096
+ *   (ALLOY_E_UNSUPPORTED).  workspace: >= alloy_moe_workspace_bytes(...) bytes.
+ */
+alloy_status alloy_gguf_moe_routed(const void* hidden, const float* router_logits,
+                                   const void* gate_up_blocks, const void* down_qweight, int32_t E,
+                                   int32_t top_k, int64_t T, int64_t H, int64_t I, void* workspace,
+                                   size_t workspace_bytes, float* y, void* stream);
+
 /* Thread-local message of the last failed call on this thread ("" if none). */
 const char* alloy_last_error(void);
 /* Library version string. */

@@ -121,9 +121,9 @@ def test_gemv_mfma(dev, fmt, M):
     for rg in (1, 2):
         y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=rg << 28).cpu().numpy()
         check(y, x, wt.W, f"{fmt} gemv_mfma M={M} rg={rg}")
-    if fmt in ("q4_k", "mlx_q4") and M <= 16:
+    if fmt in ("q4_k", "q6_k", "mlx_q4") and M <= 16:
         # every kernel explicitly: 1 = 16x16x32 tiles, 5 = 4x4x4 broadcast (Q4_K),
-        # 6 = x-stationary 16x16x32 (Q4_K), 7 = generic x-stationary (Q4_K, MLX)
+        # 6 = x-stationary 16x16x32 (Q4_K), 7 = generic x-stationary (Q4_K, Q6_K, MLX)
         for variant in ((1, 5, 6, 7) if fmt == "q4_k" else (1, 7)):
             y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=variant << 36).cpu().numpy()
             check(y, x, wt.W, f"{fmt} gemv_mfma M={M} variant={variant}")

@@ -1,5 +1,6 @@
-"""GPU parity of the MLX-4 routed-expert MoE (router, sort, grouped GEMVs, combine)
-against the oracle composition, through the C ABI."""
+"""GPU parity of the routed-expert MoE (router, sort, grouped GEMVs, combine) over
+MLX-4 and GGUF (Q4_K gate/up, Q6_K down) experts against the oracle composition,
+through the C ABI."""
 
 import numpy as np
 import pytest
@@ -106,3 +107,90 @@ def test_moe_deterministic(dev):
     a = torch.ops.alloy.mlx_moe_routed(x, lg, guq, gus, gub, dnq, dns, dnb, E, k, I)
     b = torch.ops.alloy.mlx_moe_routed(x, lg, guq, gus, gub, dnq, dns, dnb, E, k, I)
     assert torch.equal(a, b)
+
+
+# ------------------------------------------------------------------ GGUF experts
+def run_gguf_case(dev, T, E, k, H, I, seed, tokens=None, logits_dtype=torch.float32):
+    """gguf_moe_routed (Q4_K fused gate/up, Q6_K down) against the oracle composition
+    (reference role: tests/kernels/test_moe.py:123-145 with the oracle decoders)."""
+    rng = np.random.default_rng(seed)
+    gu = synth.numpy_blocks("q4_k", E * 2 * I, H, rng)
+    dn = synth.numpy_blocks("q6_k", E * H, I, rng)
+    x = synth.numpy_x(T, H, rng)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    lg = torch.from_numpy(logits).to(dev).to(logits_dtype)
+    if logits_dtype != torch.float32:
+        logits = lg.float().cpu().numpy()
+    y = torch.ops.alloy.gguf_moe_routed(torch.from_numpy(x).to(dev), lg,
+                                        torch.from_numpy(gu).reshape(E, 2 * I, -1).to(dev),
+                                        torch.from_numpy(dn).reshape(E, H, -1).to(dev), E, k, I).cpu().numpy()
+    sel = np.arange(T) if tokens is None else np.asarray(tokens)
+    idx, w = om.router_topk(logits[sel], k)
+    cache = {}
+
+    def deq(kind, e):
+        if (kind, e) not in cache:
+            if kind == "g":
+                cache[(kind, e)] = oq.dequant_q4_k(gu[e * 2 * I:(e + 1) * 2 * I], H)
+            else:
+                cache[(kind, e)] = oq.dequant_q6_k(dn[e * H:(e + 1) * H], I)
+        return cache[(kind, e)]
+
+    ref = np.zeros((len(sel), H))
+    for ti, t in enumerate(sel):
+        xt = x[t].astype(np.float64)
+        for s in range(k):
+            e = int(idx[ti, s])
+            a = deq("g", e).astype(np.float64) @ xt
+            h = om.silu(a[:I]) * a[I:]
+            ref[ti] += w[ti, s] * (deq("d", e).astype(np.float64) @ h)
+    rel = np.linalg.norm(y[sel] - ref) / np.linalg.norm(ref)
+    assert rel <= 1e-3, f"GGUF MoE T={T}: rel_fro={rel:.3e}"
+    return y
+
+
+@pytest.mark.parametrize("T", [1, 5, 21])
+def test_gguf_moe_small(dev, T):
+    # gate/up K = 512 (2 waves), down K = 256 (1 wave); full and partial tiles
+    run_gguf_case(dev, T, E=8, k=2, H=512, I=256, seed=50 + T)
+
+
+@pytest.mark.parametrize("T", [1, 16, 256])
+def test_gguf_moe_qwen3_shape(dev, T):
+    # Qwen3-MoE-like: 128 experts, top-8, H = 2048, I = 768; up to 12 tokens checked
+    tokens = None if T <= 16 else list(range(0, T, 23))
+    run_gguf_case(dev, T, E=128, k=8, H=2048, I=768, seed=200 + T, tokens=tokens)
+
+
+def test_gguf_moe_fp16_logits_and_deterministic(dev):
+    y1 = run_gguf_case(dev, 4, E=16, k=4, H=1024, I=512, seed=9, logits_dtype=torch.float16)
+    y2 = run_gguf_case(dev, 4, E=16, k=4, H=1024, I=512, seed=9, logits_dtype=torch.float16)
+    assert np.array_equal(y1, y2)
+
+
+def test_gguf_moe_block_module(dev):
+    # the block adds sigmoid(Wg x) * shared(x) to the routed output (qwen3_5.py:304-343)
+    E, k, H, I, T = 8, 2, 512, 256, 3
+    rng = np.random.default_rng(3)
+    gu = torch.from_numpy(synth.numpy_blocks("q4_k", E * 2 * I, H, rng)).reshape(E, 2 * I, -1).to(dev)
+    dn = torch.from_numpy(synth.numpy_blocks("q6_k", E * H, I, rng)).reshape(E, H, -1).to(dev)
+    experts = alloy_amd.GGUFQwen35MoeExperts(gate_up_blocks=gu, down_qweight=dn, num_experts=E, hidden_size=H,
+                                             moe_intermediate_size=I)
+
+    class Orig(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.gate = torch.nn.Linear(H, E, bias=False, dtype=torch.float16, device=dev)
+            self.experts = experts
+            self.shared_expert = torch.nn.Linear(H, H, bias=False, dtype=torch.float16, device=dev)
+            self.shared_expert_gate = torch.nn.Linear(H, 1, bias=False, dtype=torch.float16, device=dev)
+
+    orig = Orig()
+    blk = alloy_amd.GGUFQwen35MoeBlock(orig, num_experts=E, top_k=k, moe_intermediate=I)
+    x = torch.from_numpy(synth.numpy_x(T, H, rng)).to(dev)
+    out = blk(x)
+    logits = torch.nn.functional.linear(x, orig.gate.weight)
+    routed = torch.ops.alloy.gguf_moe_routed(x, logits, gu, dn, E, k, I)
+    shared = torch.sigmoid(orig.shared_expert_gate(x)) * orig.shared_expert(x)
+    assert out.shape == (T, H)
+    assert torch.equal(out, routed + shared)

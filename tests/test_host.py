@@ -12,7 +12,7 @@ import torch
 
 import alloy_amd
 from alloy_amd import _lib, formats
-from alloy_amd.modules import GGUFQ4_KLinear, GGUFQ8_0Linear, MLXQ4Linear
+from alloy_amd.modules import GGUFQ4_KLinear, GGUFQ8_0Linear, GGUFQwen35MoeExperts, MLXQ4Linear
 
 HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "alloy_amd.h"
 
@@ -121,3 +121,47 @@ def test_module_validation_matches_reference():
     m = GGUFQ4_KLinear(in_features=512, out_features=3, blocks=torch.zeros((3, 288), dtype=torch.uint8))
     assert m.blocks.shape == (3, 288)
     assert formats.row_bytes("q6_k", 4096) == 3360
+
+
+def test_gguf_moe_meta_and_validation():
+    E, H, I, T = 4, 512, 256, 3
+    gu, dn = meta((E, 2 * I, H // 256 * 144), torch.uint8), meta((E, H, I // 256 * 210), torch.uint8)
+    y = torch.ops.alloy.gguf_moe_routed(meta((T, H), torch.float16), meta((T, E), torch.float16), gu, dn, E, 2, I)
+    assert y.shape == (T, H) and y.dtype == torch.float32
+    with pytest.raises(ValueError, match="divisible by 256"):
+        torch.ops.alloy.gguf_moe_routed(meta((T, 320), torch.float16), meta((T, E), torch.float32),
+                                        meta((E, 2 * I, 180), torch.uint8), dn, E, 2, I)
+    with pytest.raises(ValueError, match="do not match"):
+        torch.ops.alloy.gguf_moe_routed(meta((T, H), torch.float16), meta((T, E), torch.float32),
+                                        meta((E, I, H // 256 * 144), torch.uint8), dn, E, 2, I)
+    with pytest.raises(TypeError):
+        torch.ops.alloy.gguf_moe_routed(meta((T, H), torch.float16), meta((T, E), torch.float32),
+                                        meta((E, 2 * I, H // 256 * 144), torch.int8), dn, E, 2, I)
+    # the C ABI: shape and size checks fail before any HIP call
+    lib = alloy_amd.lib()
+    st = lib.alloy_gguf_moe_routed(16, 16, 256, 256, E, 2, T, 320, I, 256, 1 << 20, 16, None)
+    assert st == _lib.E_SHAPE
+    st = lib.alloy_gguf_moe_routed(16, 16, 256, 256, E, 2, T, 8192, I, 256, 1 << 30, 16, None)
+    assert st == _lib.E_UNSUPPORTED
+
+
+def test_gguf_moe_modules_validate_like_reference():
+    E, H, I = 2, 512, 256
+    ok = GGUFQwen35MoeExperts(gate_up_blocks=torch.zeros((E, 2 * I, 288), dtype=torch.uint8),
+                              down_qweight=torch.zeros((E, H, 210), dtype=torch.uint8), num_experts=E,
+                              hidden_size=H, moe_intermediate_size=I)
+    assert ok.gate_up_blocks.shape == (E, 2 * I, 288)
+    with pytest.raises(RuntimeError, match="weight holder"):
+        ok()
+    with pytest.raises(ValueError, match="divisible by 256"):
+        GGUFQwen35MoeExperts(gate_up_blocks=torch.zeros((E, 2 * 100, 288), dtype=torch.uint8),
+                             down_qweight=torch.zeros((E, H, 210), dtype=torch.uint8), num_experts=E,
+                             hidden_size=H, moe_intermediate_size=100)
+    with pytest.raises(ValueError, match="do not match"):
+        GGUFQwen35MoeExperts(gate_up_blocks=torch.zeros((E, I, 288), dtype=torch.uint8),
+                             down_qweight=torch.zeros((E, H, 210), dtype=torch.uint8), num_experts=E,
+                             hidden_size=H, moe_intermediate_size=I)
+    with pytest.raises(TypeError):
+        GGUFQwen35MoeExperts(gate_up_blocks=torch.zeros((E, 2 * I, 288), dtype=torch.int8),
+                             down_qweight=torch.zeros((E, H, 210), dtype=torch.uint8), num_experts=E,
+                             hidden_size=H, moe_intermediate_size=I)
