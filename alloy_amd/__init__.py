@@ -10,11 +10,11 @@ from . import formats, synth
 from ._lib import LIB_PATH, LibraryMissing, lib
 from .modules import (GGUFQ4_KLinear, GGUFQ5_0Linear, GGUFQ6_KLinear, GGUFQ8_0Linear, GGUFQuantLinear,
                       GGUFQwen35MoeBlock, GGUFQwen35MoeExperts, MLXMoeExperts, MLXQ4Linear)
-from .ops import dequant, gguf_moe_routed, mlx_moe_routed, moe_workspace_bytes, qmm, router_topk
+from .ops import dequant, gguf_moe_routed, mlx_moe_routed, moe_workspace_bytes, qmm, qmm_glu, router_topk
 
 __all__ = [
     "LIB_PATH", "LibraryMissing", "lib", "formats", "synth",
     "GGUFQuantLinear", "GGUFQ8_0Linear", "GGUFQ5_0Linear", "GGUFQ4_KLinear", "GGUFQ6_KLinear",
     "MLXQ4Linear", "MLXMoeExperts", "GGUFQwen35MoeExperts", "GGUFQwen35MoeBlock",
-    "qmm", "dequant", "router_topk", "mlx_moe_routed", "gguf_moe_routed", "moe_workspace_bytes",
+    "qmm", "qmm_glu", "dequant", "router_topk", "mlx_moe_routed", "gguf_moe_routed", "moe_workspace_bytes",
 ]

@@ -17,6 +17,7 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent / "csrc" / "liballoy_amd.so"
 OK, E_SHAPE, E_DTYPE, E_ALIGN, E_UNSUPPORTED, E_HIP, E_ARG = range(7)
 # formats (alloy_format)
 FMT = {"q8_0": 0, "q5_0": 1, "q4_k": 2, "q6_k": 3, "mlx_q4": 4, "q8_0_split": 5, "q5_0_split": 6}
+ACT = {"silu": 0, "gelu": 1}
 # dtypes (alloy_dtype)
 DT_F32, DT_F16 = 0, 1
 # paths (alloy_path)
@@ -53,6 +54,12 @@ SIGNATURES = {
     "alloy_moe_workspace_bytes": (_sz, [_i64, _i32, _i32, _i64, _i64]),
     "alloy_mlx_moe_routed": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _i64, _vp, _sz, _vp, _vp]),
     "alloy_gguf_moe_routed": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i64, _i64, _i64, _vp, _sz, _vp, _vp]),
+    "alloy_glu_workspace_bytes": (_sz, [_i32, _i64, _i64, _i64, _i32, _i32]),
+    "alloy_qmm_glu": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _vp, _sz, _vp]),
+    "alloy_gguf_q4_k_silu": (_i32, [_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp, _sz, _vp]),
+    "alloy_gguf_q4_k_gelu": (_i32, [_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp, _sz, _vp]),
+    "alloy_mlx_q4_silu": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _vp, _sz, _vp]),
+    "alloy_gguf_q8_0_silu": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp, _sz, _vp]),
     "alloy_last_error": (ctypes.c_char_p, []),
     "alloy_version": (ctypes.c_char_p, []),
 }

@@ -248,6 +248,76 @@ alloy_status alloy_mlx_moe_routed(const void* hidden, const float* logits, const
   return hip_status(alloy::launch_mlx_moe(m, L, (hipStream_t)stream), "moe launch");
 }
 
+size_t alloy_glu_workspace_bytes(alloy_format fmt, int64_t M, int64_t N, int64_t K, int32_t group_size,
+                                 alloy_dtype x_dtype) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  if (alloy::glu_fused_supported((int)fmt, M, N, K, x_dtype == ALLOY_DT_F32, group_size)) return 0;
+  return 2 * (((size_t)M * (size_t)N * 4 + 255) & ~(size_t)255);
+}
+
+alloy_status alloy_qmm_glu(alloy_format fmt, alloy_act act, const void* gw, const void* gaux, const void* gsc,
+                           const void* gbi, const void* uw, const void* uaux, const void* usc, const void* ubi,
+                           int32_t group_size, const void* x, alloy_dtype x_dtype, void* y, alloy_dtype y_dtype,
+                           int64_t M, int64_t N, int64_t K, void* ws, size_t ws_bytes, void* stream) {
+  if (act != ALLOY_ACT_SILU && act != ALLOY_ACT_GELU_TANH) return fail(ALLOY_E_ARG, "unknown activation code %d", (int)act);
+  QArgs g, u;
+  alloy_status s = make_args((int)fmt, gw, gaux, gsc, gbi, group_size, K, g);
+  if (s != ALLOY_OK) return s;
+  if ((s = make_args((int)fmt, uw, uaux, usc, ubi, group_size, K, u)) != ALLOY_OK) return s;
+  if ((s = check_dtype(x_dtype, "activations")) != ALLOY_OK) return s;
+  if ((s = check_dtype(y_dtype, "output")) != ALLOY_OK) return s;
+  if (M < 0 || N < 0) return fail(ALLOY_E_SHAPE, "negative M=%lld or N=%lld", (long long)M, (long long)N);
+  if (N > (int64_t)1 << 31) return fail(ALLOY_E_SHAPE, "N=%lld too large", (long long)N);
+  if (M == 0 || N == 0) return ALLOY_OK;
+  if (!x || !y) return fail(ALLOY_E_ARG, "null activation or output pointer");
+  if (!aligned(x, 16)) return fail(ALLOY_E_ALIGN, "activations not 16-byte aligned");
+  if (!aligned(y, y_dtype == ALLOY_DT_F32 ? 4 : 2)) return fail(ALLOY_E_ALIGN, "output misaligned");
+  const bool xf = x_dtype == ALLOY_DT_F32, yf = y_dtype == ALLOY_DT_F32;
+  hipStream_t st = (hipStream_t)stream;
+  alloy::Opts o;
+  if (alloy::glu_fused_supported((int)fmt, M, N, K, xf, group_size))
+    return hip_status(alloy::launch_glu_fused((int)fmt, (int)act, g, u, x, xf, y, yf, M, N, o, st), "fused glu launch");
+  const size_t need = alloy_glu_workspace_bytes(fmt, M, N, K, group_size, x_dtype);
+  if (!ws || ws_bytes < need) return fail(ALLOY_E_SHAPE, "workspace %zu bytes < required %zu", ws_bytes, need);
+  if (!aligned(ws, 256)) return fail(ALLOY_E_ALIGN, "workspace not 256-byte aligned");
+  float* gf = (float*)ws;
+  float* uf = (float*)((uint8_t*)ws + need / 2);
+  s = alloy_qmm(fmt, gw, gaux, gsc, gbi, group_size, x, x_dtype, gf, ALLOY_DT_F32, M, N, K, ALLOY_PATH_AUTO, 0, stream);
+  if (s != ALLOY_OK) return s;
+  s = alloy_qmm(fmt, uw, uaux, usc, ubi, group_size, x, x_dtype, uf, ALLOY_DT_F32, M, N, K, ALLOY_PATH_AUTO, 0, stream);
+  if (s != ALLOY_OK) return s;
+  return hip_status(alloy::launch_glu_combine((int)act, gf, uf, y, yf, M * N, st), "glu combine launch");
+}
+
+alloy_status alloy_gguf_q4_k_silu(const void* x, alloy_dtype xd, const void* gate_blocks, const void* up_blocks,
+                                  void* y, alloy_dtype yd, int64_t M, int64_t N, int64_t K, void* ws,
+                                  size_t ws_bytes, void* stream) {
+  return alloy_qmm_glu(ALLOY_FMT_Q4_K, ALLOY_ACT_SILU, gate_blocks, nullptr, nullptr, nullptr, up_blocks, nullptr,
+                       nullptr, nullptr, 0, x, xd, y, yd, M, N, K, ws, ws_bytes, stream);
+}
+
+alloy_status alloy_gguf_q4_k_gelu(const void* x, alloy_dtype xd, const void* gate_blocks, const void* up_blocks,
+                                  void* y, alloy_dtype yd, int64_t M, int64_t N, int64_t K, void* ws,
+                                  size_t ws_bytes, void* stream) {
+  return alloy_qmm_glu(ALLOY_FMT_Q4_K, ALLOY_ACT_GELU_TANH, gate_blocks, nullptr, nullptr, nullptr, up_blocks,
+                       nullptr, nullptr, nullptr, 0, x, xd, y, yd, M, N, K, ws, ws_bytes, stream);
+}
+
+alloy_status alloy_mlx_q4_silu(const void* x, alloy_dtype xd, const void* gate_qweight, const void* gate_scales,
+                               const void* gate_biases, const void* up_qweight, const void* up_scales,
+                               const void* up_biases, int32_t gs, void* y, alloy_dtype yd, int64_t M, int64_t N,
+                               int64_t K, void* ws, size_t ws_bytes, void* stream) {
+  return alloy_qmm_glu(ALLOY_FMT_MLX_Q4, ALLOY_ACT_SILU, gate_qweight, nullptr, gate_scales, gate_biases, up_qweight,
+                       nullptr, up_scales, up_biases, gs, x, xd, y, yd, M, N, K, ws, ws_bytes, stream);
+}
+
+alloy_status alloy_gguf_q8_0_silu(const void* x, alloy_dtype xd, const void* gate_qweight, const void* gate_scales,
+                                  const void* up_qweight, const void* up_scales, void* y, alloy_dtype yd, int64_t M,
+                                  int64_t N, int64_t K, void* ws, size_t ws_bytes, void* stream) {
+  return alloy_qmm_glu(ALLOY_FMT_Q8_0_SPLIT, ALLOY_ACT_SILU, gate_qweight, nullptr, gate_scales, nullptr, up_qweight,
+                       nullptr, up_scales, nullptr, 0, x, xd, y, yd, M, N, K, ws, ws_bytes, stream);
+}
+
 alloy_status alloy_gguf_moe_routed(const void* hidden, const float* logits, const void* gate_up_blocks,
                                    const void* down_qweight, int32_t E, int32_t top_k, int64_t T, int64_t H,
                                    int64_t I, void* ws, size_t ws_bytes, float* y, void* stream) {

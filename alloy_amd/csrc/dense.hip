@@ -1354,6 +1354,53 @@ static hipError_t launch_gemv_xs(int fmt, const QArgs& a, const void* x, bool x_
   }
 }
 
+// ------------------------------------------------------------------ gated pair
+bool glu_fused_supported(int fmt, int64_t M, int64_t N, int64_t K, bool x_f32, int gs) {
+  if (x_f32 || M < 1 || M > 16 || K % 256 || K > 4096 || N >= (1ll << 31)) return false;
+  if (fmt == F_Q4_K) return true;
+  return fmt == F_MLX && gs >= 32 && gs <= 256 && !(gs & (gs - 1));
+}
+
+hipError_t launch_glu_fused(int fmt, int act, const QArgs& g, const QArgs& u, const void* x, bool x_f32,
+                            void* y, bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st) {
+  if (!glu_fused_supported(fmt, M, N, g.K, x_f32, g.gs)) return hipErrorNotSupported;
+  XsJob j{};
+  j.a = g;
+  j.a2 = u;
+  j.act = act;
+  j.x = x;
+  j.xbytes = (uint32_t)(M * g.K * 2);
+  j.xld = g.K;
+  j.M = (int)M;
+  j.N = (int)N;
+  j.y = y;
+  j.y_f32 = y_f32;
+  const int64_t cap = o.grid_cap > 0 ? o.grid_cap : 0;
+  if (fmt == F_Q4_K) return launch_xs<XsQ4K, 3>(j, 0, cap, 0, st);
+  j.sb = (uint32_t)(g.K / g.gs * 2);
+  switch (g.gs) {
+    case 32: return launch_xs<XsMLX<0>, 3>(j, 0, cap, 0, st);
+    case 64: return launch_xs<XsMLX<1>, 3>(j, 0, cap, 0, st);
+    case 128: return launch_xs<XsMLX<2>, 3>(j, 0, cap, 0, st);
+    default: return launch_xs<XsMLX<3>, 3>(j, 0, cap, 0, st);
+  }
+}
+
+template <typename YT>
+__global__ __launch_bounds__(256) void k_glu_combine(const float* g, const float* u, YT* y, int64_t n, int act) {
+  for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    y[i] = (YT)xs_f32_product(xs_act(act, g[i]), u[i]);   // fp32 product, then the conversion
+}
+
+hipError_t launch_glu_combine(int act, const float* g, const float* u, void* y, bool y_f32, int64_t n,
+                              hipStream_t st) {
+  const int64_t blocks = (n + 255) / 256;
+  const dim3 grid((unsigned)(blocks < 4096 ? blocks : 4096));
+  if (y_f32) hipLaunchKernelGGL(k_glu_combine<float>, grid, dim3(256), 0, st, g, u, (float*)y, n, act);
+  else hipLaunchKernelGGL(k_glu_combine<f16>, grid, dim3(256), 0, st, g, u, (f16*)y, n, act);
+  return hipGetLastError();
+}
+
 hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
                             bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;

@@ -33,6 +33,15 @@ hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, 
 hipError_t launch_gemm(int fmt, const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32,
                        int64_t M, int64_t N, const Opts& o, hipStream_t st);
 
+// Gated pair y = act(x G^T) * (x U^T) (act 0 silu, 1 gelu in tanh form): one fused
+// launch for M <= 16 when glu_fused_supported(), else two products into fp32
+// buffers and launch_glu_combine over them.
+bool glu_fused_supported(int fmt, int64_t M, int64_t N, int64_t K, bool x_f32, int gs);
+hipError_t launch_glu_fused(int fmt, int act, const QArgs& g, const QArgs& u, const void* x, bool x_f32,
+                            void* y, bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st);
+hipError_t launch_glu_combine(int act, const float* g, const float* u, void* y, bool y_f32, int64_t n,
+                              hipStream_t st);
+
 // The v_dot2 GEMV gives each thread at most 2 decode units of a 256-thread row:
 // K <= 512 units per row.
 inline int64_t max_k_dot2(int fmt) { return fmt == F_Q6_K ? 512 * 64 : 512 * 32; }

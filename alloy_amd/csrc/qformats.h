@@ -104,6 +104,7 @@ __device__ __forceinline__ uint32_t lshl_or(uint32_t a, uint32_t b) {           
 #define ALLOY_RSRC_DW3 0x00020000   // gfx9 buffer descriptor word 3: 32-bit data format
 struct Src {
   __amdgpu_buffer_rsrc_t w, aux, s, b;
+  __device__ Src() {}
   __device__ Src(const QArgs& a, uint32_t wbytes, uint32_t sbytes) {
     w = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, (int)wbytes, ALLOY_RSRC_DW3);
     aux = __builtin_amdgcn_make_buffer_rsrc((void*)a.aux, (short)0, a.aux ? (int)wbytes : 0, ALLOY_RSRC_DW3);

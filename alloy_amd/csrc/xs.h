@@ -273,11 +273,15 @@ struct XsQ6K {
 //         p0 .. p0+cnt); token slot t gathers x[token t of the record]; weight rows
 //         e*2N + n (gate) and e*2N + N + n (up); h[p0+t, n] = silu(gate) * up (fp32).
 // MODE 2: routed down: x = h[p0+t] (fp32); weight rows e*N + n; part[p0+t, n] (fp32).
+// MODE 3: dense gated pair y[t, n] = act(x[t] . G[n]) * (x[t] . U[n]) for t < M, with
+//         G = a and U = a2 (y fp16 or fp32).
 //         Each token's activations enter the MFMA as fp16 after a power-of-two
 //         scaling that puts the token's largest |h| in [2^14, 2^15) (fp16 range,
 //         11-bit precision whatever the magnitude); the result is scaled back.
 struct XsJob {
-  QArgs a;                 // whole matrix (all experts for MODE 1/2)
+  QArgs a;                 // whole matrix (all experts for MODE 1/2; the gate for MODE 3)
+  QArgs a2;                // MODE 3: the up matrix (same format and shape as a)
+  int act;                 // MODE 3: 0 silu, 1 gelu (tanh form)
   uint32_t sb;             // bytes per row of scales / biases (MLX), else 0
   const void* x;           // fp16 (MODE 0/1) or fp32 (MODE 2) activations
   uint32_t xbytes;         // bytes of x readable (bounds of the activation buffer)
@@ -292,6 +296,23 @@ struct XsJob {
   float* part;             // MODE 2 output
   int W;                   // waves per workgroup (set by the launcher)
 };
+
+// a * b rounded to fp32.  The empty asm (no instruction) pins the fp32 value: without
+// it the compiler fuses the product with a following fp16 conversion (v_fma_mix,
+// one rounding), which can differ from rounding the fp32 output.
+__device__ __forceinline__ float xs_f32_product(float a, float b) {
+  float p = a * b;
+  asm volatile("" : "+v"(p));
+  return p;
+}
+
+// Gate activations of the fused gated pair: silu(v) = v / (1 + e^-v); gelu in the
+// tanh form 0.5 v (1 + tanh(clamp(sqrt(2/pi) (v + 0.044715 v^3), -10, 10))).
+__device__ __forceinline__ float xs_act(int act, float v) {
+  if (act == 0) return v * __builtin_amdgcn_rcpf(1.f + __expf(-v));
+  const float u = fminf(fmaxf(0.7978845608028654f * (v + 0.044715f * v * v * v), -10.f), 10.f);
+  return 0.5f * v * (1.f + tanhf(u));
+}
 
 template <int I, int N, class Fn>
 __device__ __forceinline__ void xs_static_for(Fn&& f) {
@@ -313,7 +334,7 @@ __device__ __forceinline__ void xs_static_for(Fn&& f) {
 // + tsc[16] for MODE 2) floats.
 template <class P, int MODE, int NS, int TT, int RT, bool PIPE, class YT>
 __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
-  constexpr int NM = MODE == 1 ? 2 : 1;          // weight matrices per output
+  constexpr int NM = (MODE == 1 || MODE == 3) ? 2 : 1;   // weight matrices per output
   constexpr int UPW = NS / 8;                    // units per wave
   constexpr int NCH = P::NCH;                    // chains per unit
   using Raw = typename P::Raw;
@@ -333,7 +354,7 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
 
   int cnt = j.M, p0 = 0, tok = 0;
   int64_t row0 = 0;                                      // first weight row of the block
-  if constexpr (MODE != 0) {
+  if constexpr (MODE == 1 || MODE == 2) {
     // the tile count and the record are read together (records exist for every
     // grid row; those past the count are not used).  The uniform values are moved to
     // scalar registers: a loop that reads a vector register filled by a memory load
@@ -349,12 +370,18 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
     if (tile >= nt) return;                              // uniform per workgroup
     row0 = (int64_t)e * (NM * j.N);
   }
-  QArgs ab = j.a;
-  ab.w += row0 * j.a.rb;
-  if (ab.s) ab.s += row0 * (j.sb / 2);
-  if (ab.b) ab.b += row0 * (j.sb / 2);
-  const uint32_t rows = (uint32_t)(NM * j.N);
-  const Src src(ab, rows * (uint32_t)j.a.rb, rows * j.sb);
+  // one buffer view per weight matrix, N rows each (rows past N read zero)
+  auto rows_from = [&](const QArgs& q, int64_t r0) {
+    QArgs o = q;
+    o.w += r0 * q.rb;
+    if (o.s) o.s += r0 * (j.sb / 2);
+    if (o.b) o.b += r0 * (j.sb / 2);
+    return Src(o, (uint32_t)j.N * (uint32_t)q.rb, (uint32_t)j.N * j.sb);
+  };
+  Src src[NM];
+  src[0] = rows_from(j.a, row0);
+  if constexpr (MODE == 1) src[1] = rows_from(j.a, row0 + j.N);   // up rows follow the gate rows
+  if constexpr (MODE == 3) src[1] = rows_from(j.a2, 0);
   const uint32_t rb = (uint32_t)j.a.rb;
   const int ntiles16 = (j.N + 15) >> 4;
   const int stride = (int)gridDim.x * RT;
@@ -365,12 +392,11 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
     for (int r = 0; r < RT; ++r) {
       const bool in = t + r < ntiles16;
       const uint32_t n = (uint32_t)((t + r) * 16 + n16);
+      const uint32_t rw = in ? n * rb : 0x80000000u, rs = in ? n * j.sb : 0x80000000u;
 #pragma unroll
       for (int mi = 0; mi < NM; ++mi) {
-        const uint32_t row = n + (uint32_t)(mi * j.N);
-        const uint32_t rw = in ? row * rb : 0x80000000u, rs = in ? row * j.sb : 0x80000000u;
 #pragma unroll
-        for (int u = 0; u < UPW; ++u) P::load(src, rw, rs, u0 + u, kq, raw[r][mi][u]);
+        for (int u = 0; u < UPW; ++u) P::load(src[mi], rw, rs, u0 + u, kq, raw[r][mi][u]);
       }
     }
   };
@@ -471,6 +497,8 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
       }
       if constexpr (MODE == 0) {
         ((YT*)j.y)[(int64_t)tk * j.N + n] = (YT)v0;
+      } else if constexpr (MODE == 3) {
+        ((YT*)j.y)[(int64_t)tk * j.N + n] = (YT)xs_f32_product(xs_act(j.act, v0), v1);
       } else if constexpr (MODE == 1) {
         j.h[(int64_t)(p0 + tk) * j.N + n] = v0 * __builtin_amdgcn_rcpf(1.f + __expf(-v0)) * v1;
       } else {
@@ -552,21 +580,22 @@ int xs_resident_per_cu(Kern kern, int W, size_t lds) {
 // output tiles per column tile (0: chosen here).
 template <class P, int MODE>
 hipError_t launch_xs(const XsJob& j, int64_t tiles_y, int64_t cap, int rt, hipStream_t st) {
-  constexpr int NM = MODE == 1 ? 2 : 1;
+  constexpr int NM = (MODE == 1 || MODE == 3) ? 2 : 1;
+  constexpr bool DENSE = MODE == 0 || MODE == 3;
   const int K = j.a.K;
   if (K <= 0 || K % 256 || j.M > 16 || j.N <= 0) return hipErrorNotSupported;
-  const uint64_t rows = (uint64_t)NM * (uint64_t)j.N + 16u;
+  const uint64_t rows = (uint64_t)j.N + 16u;
   if (rows * (uint64_t)j.a.rb >= (1ull << 31) || rows * j.sb >= (1ull << 31) || j.xbytes >= (1u << 31))
     return hipErrorNotSupported;
   const int KS = K / 32;
   const int ns = KS <= 8 * 16 ? 8 : KS <= 16 * 16 ? 16 : 0;   // at most 16 waves
-  if (!ns || ((MODE == 1 || !P::WIDE) && ns == 16)) return hipErrorNotSupported;   // (registers)
-  if (MODE != 0 && tiles_y > 65535) return hipErrorNotSupported;
-  if (MODE != 0 && tiles_y <= 0) return hipSuccess;
+  if (!ns || ((NM == 2 || !P::WIDE) && ns == 16)) return hipErrorNotSupported;   // (registers)
+  if (!DENSE && tiles_y > 65535) return hipErrorNotSupported;
+  if (!DENSE && tiles_y <= 0) return hipSuccess;
   const int W = (KS + ns - 1) / ns;
   const int64_t tiles = (j.N + 15) / 16;
   // 16 sub-blocks per wave leave registers for one tile in flight only
-  rt = (ns == 16 || MODE != 0 || rt < 2 || !P::WIDE) ? 1 : 2;
+  rt = (ns == 16 || MODE != 0 || rt < 2 || !P::WIDE) ? 1 : 2;   // (two tiles: MODE 0 only)
   const int64_t groups = (tiles + rt - 1) / rt;
   const size_t lds = (size_t)W * (ns / 8) * P::NCH * 16 * 4 + (size_t)W * rt * 64 * 4 * NM * 4 +
                      (MODE == 2 ? (size_t)(W * 16 + 16) * 4 : 0);
@@ -584,7 +613,7 @@ hipError_t launch_xs(const XsJob& j, int64_t tiles_y, int64_t cap, int rt, hipSt
       const int64_t c = cap > 0 ? cap : (int64_t)xs_resident_per_cu(kern, W, lds) * xs_cu_count();
       gx = groups < c ? groups : c;
     }
-    const dim3 grid((unsigned)gx, MODE == 0 ? 1u : (unsigned)tiles_y), block((unsigned)(64 * W));
+    const dim3 grid((unsigned)gx, DENSE ? 1u : (unsigned)tiles_y), block((unsigned)(64 * W));
     XsJob jw = j;
     jw.W = W;
     hipLaunchKernelGGL(kern, grid, block, lds, st, jw);
@@ -608,6 +637,15 @@ hipError_t launch_xs(const XsJob& j, int64_t tiles_y, int64_t cap, int rt, hipSt
       }
       if (many(k_gemv_xs<P, 0, 8, TT, 1, false, YT>)) return go(k_gemv_xs<P, 0, 8, TT, 1, true, YT>, true);
       return go(k_gemv_xs<P, 0, 8, TT, 1, false, YT>, false);
+    };
+    if (j.y_f32) return tt == 1 ? pick(I1(), 0.f) : tt == 2 ? pick(I2(), 0.f) : pick(I4(), 0.f);
+    return tt == 1 ? pick(I1(), (f16)0) : tt == 2 ? pick(I2(), (f16)0) : pick(I4(), (f16)0);
+  } else if constexpr (MODE == 3) {
+    auto pick = [&](auto ttc, auto yt) -> hipError_t {
+      constexpr int TT = decltype(ttc)::value;
+      using YT = decltype(yt);
+      if (many(k_gemv_xs<P, 3, 8, TT, 1, false, YT>)) return go(k_gemv_xs<P, 3, 8, TT, 1, true, YT>, true);
+      return go(k_gemv_xs<P, 3, 8, TT, 1, false, YT>, false);
     };
     if (j.y_f32) return tt == 1 ? pick(I1(), 0.f) : tt == 2 ? pick(I2(), 0.f) : pick(I4(), 0.f);
     return tt == 1 ? pick(I1(), (f16)0) : tt == 2 ? pick(I2(), (f16)0) : pick(I4(), (f16)0);

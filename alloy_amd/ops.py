@@ -187,6 +187,86 @@ def mlx_moe_routed(hidden, router_logits, gate_up_qweight, gate_up_scales, gate_
     return y
 
 
+def _glu_workspace(fmt: str, x: torch.Tensor, M: int, N: int, K: int, gs: int, dev) -> tuple:
+    need = int(_lib.lib().alloy_glu_workspace_bytes(_lib.FMT[fmt], M, N, K, gs, _dt(x.dtype, "activations")))
+    ws = torch.empty(need, dtype=torch.uint8, device=dev) if need else None
+    return ws, need
+
+
+def qmm_glu(fmt: str, act: str, x: torch.Tensor, gate: dict, up: dict, *, group_size: int = 0,
+            N: int | None = None, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """y = act(x @ dequant(gate)^T) * (x @ dequant(up)^T) through ``alloy_qmm_glu``;
+    ``gate`` / ``up``: dicts with ``w`` and optional ``aux``, ``scales``, ``biases``."""
+    M, K = _check_act(x)
+    N = gate["w"].shape[0] if N is None else N
+    dev = _same_device(x, gate["w"], up["w"])
+    x = x.contiguous()
+    y = torch.empty((M, N), dtype=out_dtype or x.dtype, device=dev)
+    ws, need = _glu_workspace(fmt, x, M, N, K, group_size, dev)
+    g = [_p(gate.get(k)) for k in ("w", "aux", "scales", "biases")]
+    u = [_p(up.get(k)) for k in ("w", "aux", "scales", "biases")]
+    with torch.cuda.device(dev):
+        _lib.call("alloy_qmm_glu", _lib.FMT[fmt], _lib.ACT[act], *g, *u, group_size, _p(x), _dt(x.dtype, "activations"),
+                  _p(y), _dt(y.dtype, "output"), M, N, K, _p(ws), need, _stream(dev))
+    return y
+
+
+def _same_shape(a: torch.Tensor, b: torch.Tensor, what: str) -> None:
+    if tuple(a.shape) != tuple(b.shape) or a.dtype != b.dtype:
+        raise ValueError(f"{what}: gate and up buffers differ ({tuple(a.shape)} vs {tuple(b.shape)})")
+
+
+def _run_glu(name: str, fmt: str, activations, gate_bufs, up_bufs, M, N, K, gs=0, gs_arg=False):
+    dev = _same_device(activations, *gate_bufs, *up_bufs)
+    x = activations.contiguous()
+    y = _empty_out(x, N)
+    if M and N:
+        ws, need = _glu_workspace(fmt, x, M, N, K, gs, dev)
+        extra = (gs,) if gs_arg else ()
+        with torch.cuda.device(dev):
+            _lib.call(name, _p(x), _dt(x.dtype, "activations"), *[_p(b.contiguous()) for b in gate_bufs],
+                      *[_p(b.contiguous()) for b in up_bufs], *extra, _p(y), _dt(y.dtype, "output"), M, N, K,
+                      _p(ws), need, _stream(dev))
+    return y
+
+
+def shape_glu_q4_k(activations, gate_blocks, up_blocks):
+    _same_shape(gate_blocks, up_blocks, "gguf_q4_k glu")
+    return shape_gguf_blocks("q4_k", activations, gate_blocks)
+
+
+def shape_glu_mlx(activations, gq, gsc, gb, uq, usc, ub):
+    for a, b in ((gq, uq), (gsc, usc), (gb, ub)):
+        _same_shape(a, b, "mlx_q4_silu")
+    return shape_mlx(activations, gq, gsc, gb)
+
+
+def shape_glu_q8_0(activations, gq, gsc, uq, usc):
+    for a, b in ((gq, uq), (gsc, usc)):
+        _same_shape(a, b, "gguf_q8_0_silu")
+    return shape_q8_0(activations, gq, gsc)
+
+
+def _q4_k_silu(activations, gate_blocks, up_blocks):
+    M, N, K = shape_glu_q4_k(activations, gate_blocks, up_blocks)
+    return _run_glu("alloy_gguf_q4_k_silu", "q4_k", activations, [gate_blocks], [up_blocks], M, N, K)
+
+
+def _q4_k_gelu(activations, gate_blocks, up_blocks):
+    M, N, K = shape_glu_q4_k(activations, gate_blocks, up_blocks)
+    return _run_glu("alloy_gguf_q4_k_gelu", "q4_k", activations, [gate_blocks], [up_blocks], M, N, K)
+
+
+def _mlx_silu(activations, gq, gsc, gb, uq, usc, ub):
+    M, N, K, gs = shape_glu_mlx(activations, gq, gsc, gb, uq, usc, ub)
+    return _run_glu("alloy_mlx_q4_silu", "mlx_q4", activations, [gq, gsc, gb], [uq, usc, ub], M, N, K, gs, True)
+
+
+def _q8_0_silu(activations, gq, gsc, uq, usc):
+    M, N, K = shape_glu_q8_0(activations, gq, gsc, uq, usc)
+    return _run_glu("alloy_gguf_q8_0_silu", "q8_0_split", activations, [gq, gsc], [uq, usc], M, N, K)
+
+
 def gguf_moe_routed(hidden, router_logits, gate_up_blocks, down_qweight, num_experts: int, top_k: int,
                     moe_intermediate: int, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Routed GGUF experts (Q4_K fused gate/up, Q6_K down) -> float32 (T, H), like the
@@ -267,6 +347,17 @@ _LIB.define("batched_mlx_q4_mm(Tensor activations, Tensor[] qweights, Tensor[] s
 # wire-block Q8_0 / Q5_0 (the raw GGUF blob; the reference only has the split ops)
 _LIB.define("gguf_q8_0_blocks_mm(Tensor activations, Tensor blocks) -> Tensor")
 _LIB.define("gguf_q5_0_blocks_mm(Tensor activations, Tensor blocks) -> Tensor")
+# fused gated pairs (reference custom_ops.py:53-58, 79-82, 108-111)
+_LIB.define("gguf_q4_k_silu(Tensor activations, Tensor gate_blocks, Tensor up_blocks) -> Tensor")
+_LIB.define("gguf_q4_k_gelu(Tensor activations, Tensor gate_blocks, Tensor up_blocks) -> Tensor")
+_LIB.define(
+    "mlx_q4_silu(Tensor activations, Tensor gate_qweight, Tensor gate_scales, "
+    "Tensor gate_biases, Tensor up_qweight, Tensor up_scales, Tensor up_biases) -> Tensor"
+)
+_LIB.define(
+    "gguf_q8_0_silu(Tensor activations, Tensor gate_qweight, Tensor gate_scales, "
+    "Tensor up_qweight, Tensor up_scales) -> Tensor"
+)
 # GGUF routed experts (reference custom_ops.py:59-66)
 _LIB.define(
     "gguf_moe_routed(Tensor hidden, Tensor router_logits, Tensor gate_up_blocks, "
@@ -386,6 +477,20 @@ for _name, _single in _BATCHED.items():
 
 torch.library.impl(_LIB, "mlx_moe_routed", "CUDA")(mlx_moe_routed)
 torch.library.impl(_LIB, "gguf_moe_routed", "CUDA")(gguf_moe_routed)
+
+_GLU = {
+    "gguf_q4_k_silu": (_q4_k_silu, shape_glu_q4_k),
+    "gguf_q4_k_gelu": (_q4_k_gelu, shape_glu_q4_k),
+    "mlx_q4_silu": (_mlx_silu, shape_glu_mlx),
+    "gguf_q8_0_silu": (_q8_0_silu, shape_glu_q8_0),
+}
+for _name, (_fn, _shape) in _GLU.items():
+    torch.library.impl(_LIB, _name, "CUDA")(_fn)
+
+    def _glu_meta(*args, _s=_shape):
+        return _empty_out(args[0], _s(*args)[1])
+
+    torch.library.impl(_LIB, _name, "Meta")(_glu_meta)
 
 
 @torch.library.impl(_LIB, "gguf_moe_routed", "Meta")

@@ -54,6 +54,11 @@ typedef enum {
 
 typedef enum { ALLOY_DT_F32 = 0, ALLOY_DT_F16 = 1 } alloy_dtype;
 
+/* Gate activation of the fused gated pair: silu(v) = v / (1 + exp(-v)); gelu in the
+ * tanh form 0.5 v (1 + tanh(clamp(sqrt(2/pi) (v + 0.044715 v^3), -10, 10)))
+ * (packages/alloy-metal/src/alloy/_compiler/trace/__init__.py:432-450). */
+typedef enum { ALLOY_ACT_SILU = 0, ALLOY_ACT_GELU_TANH = 1 } alloy_act;
+
 typedef enum {
   ALLOY_PATH_AUTO = 0,      /* M==1 -> GEMV (v_dot2); M<=16 -> MFMA GEMV; else MFMA GEMM */
   ALLOY_PATH_GEMV = 1,      /* v_dot2 GEMV, one x row per grid row (any M) */
@@ -166,6 +171,45 @@ alloy_status alloy_mlx_moe_routed(const void* hidden, const float* router_logits
                                   int32_t group_size, int32_t E, int32_t top_k, int64_t T,
                                   int64_t H, int64_t I, void* workspace, size_t workspace_bytes,
                                   float* y, void* stream);
+
+/*
+ * Fused gated pair y[M,N] = act(x G^T) * (x U^T) over two weight matrices of one
+ * format (each passed like alloy_qmm's w / aux / scales / biases) — the reference's
+ * *_silu / *_gelu ops (custom_ops.py:53-58, 79-82, 108-111; kernels
+ * packages/alloy-metal/src/alloy/std/quant.py:356-759, 1456-1940, 2833-2887).
+ * For M <= 16 (Q4_K, MLX with a power-of-two group size <= 256, K % 256 == 0,
+ * K <= 4096, fp16 x) one launch reads both matrices and applies the activation in
+ * its epilogue and no workspace is needed; otherwise the two products go to fp32
+ * workspace buffers and a combine kernel writes y.  workspace: >=
+ * alloy_glu_workspace_bytes(...) bytes, 256-byte aligned (may be NULL when that is 0).
+ */
+size_t alloy_glu_workspace_bytes(alloy_format fmt, int64_t M, int64_t N, int64_t K, int32_t group_size,
+                                 alloy_dtype x_dtype);
+alloy_status alloy_qmm_glu(alloy_format fmt, alloy_act act, const void* gate_w, const void* gate_aux,
+                           const void* gate_scales, const void* gate_biases, const void* up_w,
+                           const void* up_aux, const void* up_scales, const void* up_biases,
+                           int32_t group_size, const void* x, alloy_dtype x_dtype, void* y,
+                           alloy_dtype y_dtype, int64_t M, int64_t N, int64_t K, void* workspace,
+                           size_t workspace_bytes, void* stream);
+/* gguf_q4_k_silu / gguf_q4_k_gelu(activations, gate_blocks, up_blocks) — custom_ops.py:53-58 */
+alloy_status alloy_gguf_q4_k_silu(const void* x, alloy_dtype x_dtype, const void* gate_blocks,
+                                  const void* up_blocks, void* y, alloy_dtype y_dtype, int64_t M, int64_t N,
+                                  int64_t K, void* workspace, size_t workspace_bytes, void* stream);
+alloy_status alloy_gguf_q4_k_gelu(const void* x, alloy_dtype x_dtype, const void* gate_blocks,
+                                  const void* up_blocks, void* y, alloy_dtype y_dtype, int64_t M, int64_t N,
+                                  int64_t K, void* workspace, size_t workspace_bytes, void* stream);
+/* mlx_q4_silu(activations, gate_qweight, gate_scales, gate_biases, up_qweight, up_scales,
+ * up_biases) — custom_ops.py:79-82 */
+alloy_status alloy_mlx_q4_silu(const void* x, alloy_dtype x_dtype, const void* gate_qweight,
+                               const void* gate_scales, const void* gate_biases, const void* up_qweight,
+                               const void* up_scales, const void* up_biases, int32_t group_size, void* y,
+                               alloy_dtype y_dtype, int64_t M, int64_t N, int64_t K, void* workspace,
+                               size_t workspace_bytes, void* stream);
+/* gguf_q8_0_silu(activations, gate_qweight, gate_scales, up_qweight, up_scales) — custom_ops.py:108-111 */
+alloy_status alloy_gguf_q8_0_silu(const void* x, alloy_dtype x_dtype, const void* gate_qweight,
+                                  const void* gate_scales, const void* up_qweight, const void* up_scales,
+                                  void* y, alloy_dtype y_dtype, int64_t M, int64_t N, int64_t K,
+                                  void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Routed-expert MoE block over GGUF experts — torch.ops.alloy.gguf_moe_routed

@@ -11,6 +11,7 @@ Modules
 ``oracle.quant``  block decoders (Q8_0, Q5_0, Q4_K, Q6_K, MLX 4-bit affine),
                   the reference's split-layout repacks, fp64 reference matmul.
 ``oracle.moe``    router top-k + softmax, per-expert MoE composition.
+``oracle.glu``    fused gated pair act(x G^T) * (x U^T), silu and tanh-form gelu.
 
 Parity pinning (how each function is checked, beyond retyping it):
 
@@ -26,6 +27,8 @@ Parity pinning (how each function is checked, beyond retyping it):
 * router: checked against the HF formula softmax -> top-k -> renormalise and the
   lowest-index tie rule on constructed ties.
 * MoE: checked against a brute-force per-token loop over experts.
+* gated pair: silu against scipy's logistic function, tanh-form gelu against the
+  exact erf GELU within its approximation error, the pair against a brute-force loop.
 
 No function here is "parity unpinned".
 """

@@ -195,3 +195,34 @@ def test_moe_composition_brute_force():
             for j in range(H):
                 acc[j] += w[t, s] * sum(float(dn[e, j, i]) * h[i] for i in range(I))
         assert np.allclose(y[t], acc, rtol=1e-10, atol=1e-10)
+
+
+def test_glu_activations_pinned():
+    import math
+    from scipy.special import expit
+    from oracle import glu as og
+    v = np.linspace(-30.0, 30.0, 601)
+    assert np.allclose(og.silu(v), v * expit(v), rtol=1e-12, atol=1e-300)
+    # tanh-form GELU vs the exact erf GELU: the approximation is within 5e-4 absolute
+    exact = np.array([0.5 * t * (1.0 + math.erf(t / math.sqrt(2.0))) for t in v])
+    assert np.max(np.abs(og.gelu_tanh(v) - exact)) < 5e-4
+    assert og.gelu_tanh(np.array([0.0]))[0] == 0.0
+    assert abs(og.gelu_tanh(np.array([12.0]))[0] - 12.0) < 1e-6     # the clamp: tanh(10) = 1 - 4e-9
+    assert abs(og.gelu_tanh(np.array([-12.0]))[0]) < 1e-7        # 0.5 v (1 - tanh(10))
+
+
+def test_glu_pair_brute_force():
+    from oracle import glu as og
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((2, 6)).astype(np.float16)
+    g = rng.standard_normal((3, 6)).astype(np.float32)
+    u = rng.standard_normal((3, 6)).astype(np.float32)
+    for act in ("silu", "gelu"):
+        y = og.glu(x, g, u, act)
+        for m in range(2):
+            for n in range(3):
+                a = sum(float(x[m, k]) * float(g[n, k]) for k in range(6))
+                b = sum(float(x[m, k]) * float(u[n, k]) for k in range(6))
+                fa = a / (1.0 + np.exp(-a)) if act == "silu" else \
+                    0.5 * a * (1.0 + np.tanh(np.clip(0.7978845608028654 * (a + 0.044715 * a ** 3), -10, 10)))
+                assert abs(y[m, n] - fa * b) < 1e-12 * max(1.0, abs(fa * b))
