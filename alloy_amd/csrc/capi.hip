@@ -248,6 +248,64 @@ alloy_status alloy_mlx_moe_routed(const void* hidden, const float* logits, const
   return hip_status(alloy::launch_mlx_moe(m, L, (hipStream_t)stream), "moe launch");
 }
 
+alloy_status alloy_qmm_batched(alloy_format fmt, int32_t n, const void* const* w, const void* const* aux,
+                               const void* const* scales, const void* const* biases, const int64_t* N,
+                               int32_t group_size, const void* x, alloy_dtype x_dtype, void* const* y,
+                               alloy_dtype y_dtype, int64_t M, int64_t K, void* stream) {
+  if (n < 0) return fail(ALLOY_E_ARG, "negative matrix count %d", n);
+  if (n == 0) return ALLOY_OK;
+  if (!w || !N || !y) return fail(ALLOY_E_ARG, "null pointer table");
+  alloy_status s;
+  if ((s = check_dtype(x_dtype, "activations")) != ALLOY_OK) return s;
+  if ((s = check_dtype(y_dtype, "output")) != ALLOY_OK) return s;
+  if (M < 0 || K <= 0) return fail(ALLOY_E_SHAPE, "bad M=%lld or K=%lld", (long long)M, (long long)K);
+  const bool xf = x_dtype == ALLOY_DT_F32, yf = y_dtype == ALLOY_DT_F32;
+  // one launch per group of up to kMaxBatch matrices (M = 1, wave-row kernel);
+  // otherwise (or for a shape that kernel does not take) one alloy_qmm per matrix
+  auto single = [&](int i) -> alloy_status {
+    return alloy_qmm(fmt, w[i], aux ? aux[i] : nullptr, scales ? scales[i] : nullptr, biases ? biases[i] : nullptr,
+                     group_size, x, x_dtype, y[i], y_dtype, M, N[i], K, ALLOY_PATH_AUTO, 0, stream);
+  };
+  alloy::WaveBatch b{};
+  int which[alloy::kMaxBatch];
+  auto flush = [&]() -> alloy_status {
+    if (b.n == 0) return ALLOY_OK;
+    const hipError_t e = alloy::launch_gemv_batched((int)fmt, b, x, xf, yf, alloy::Opts{}, (hipStream_t)stream);
+    const int cnt = b.n;
+    b.n = 0;
+    if (e == hipSuccess) return ALLOY_OK;
+    if (e != hipErrorNotSupported) return hip_status(e, "batched gemv launch");
+    (void)hipGetLastError();
+    for (int k = 0; k < cnt; ++k) {
+      const alloy_status r = single(which[k]);
+      if (r != ALLOY_OK) return r;
+    }
+    return ALLOY_OK;
+  };
+  const bool one_launch = M == 1 && !xf && K <= alloy::max_k_dot2((int)fmt);
+  for (int i = 0; i < n; ++i) {
+    if (N[i] < 0 || N[i] >= ((int64_t)1 << 31)) return fail(ALLOY_E_SHAPE, "bad N=%lld of matrix %d", (long long)N[i], i);
+    if (N[i] == 0 || M == 0) continue;         // (an empty matrix may have no buffer at all)
+    QArgs a;
+    if ((s = make_args((int)fmt, w[i], aux ? aux[i] : nullptr, scales ? scales[i] : nullptr,
+                       biases ? biases[i] : nullptr, group_size, K, a)) != ALLOY_OK) return s;
+    if (!x || !y[i]) return fail(ALLOY_E_ARG, "null activation or output pointer");
+    if (!aligned(x, 16)) return fail(ALLOY_E_ALIGN, "activations not 16-byte aligned");
+    if (!aligned(y[i], yf ? 4 : 2)) return fail(ALLOY_E_ALIGN, "output %d misaligned", i);
+    if (!one_launch) {
+      if ((s = single(i)) != ALLOY_OK) return s;
+      continue;
+    }
+    which[b.n] = i;
+    b.a[b.n] = a;
+    b.y[b.n] = y[i];
+    b.ldy[b.n] = N[i];
+    b.N[b.n] = (int)N[i];
+    if (++b.n == alloy::kMaxBatch && (s = flush()) != ALLOY_OK) return s;
+  }
+  return flush();
+}
+
 size_t alloy_glu_workspace_bytes(alloy_format fmt, int64_t M, int64_t N, int64_t K, int32_t group_size,
                                  alloy_dtype x_dtype) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;

@@ -220,9 +220,18 @@ __device__ __forceinline__ float dpp_sum_rows(float v, int lshift) {
   return lshift == 4 ? v : lshift == 5 ? s32 : s64;
 }
 
-template <class F, int UPT, int D, typename XT, typename YT>
-__global__ __launch_bounds__(256) void k_gemv_w(QArgs a, uint32_t sb, const XT* x, YT* y,
-                                                int64_t ldy, int N, int lshift) {
+template <class F, int UPT, int D, typename XT, typename YT, int NB>
+__global__ __launch_bounds__(256) void k_gemv_w(WaveBatchT<NB> bt, uint32_t sb, const XT* x, int lshift) {
+  // this workgroup's matrix: the batch entry whose block range holds blockIdx.x
+  // (uniform; single-matrix launches are batches of one, NB = 1)
+  int mi = 0;
+#pragma unroll
+  for (int i = 1; i < NB; ++i) mi = (i < bt.n && (int)blockIdx.x >= bt.b0[i]) ? i : mi;
+  const QArgs a = bt.a[mi];
+  YT* const y = (YT*)bt.y[mi];
+  const int64_t ldy = bt.ldy[mi];
+  const int N = bt.N[mi];
+  const int bx = (int)blockIdx.x - bt.b0[mi], gx = bt.b0[mi + 1] - bt.b0[mi];
   const int L = 1 << lshift;
   const int t = threadIdx.x, li = t & (L - 1), slot = t >> lshift;
   const int R = blockDim.x >> lshift;
@@ -246,8 +255,8 @@ __global__ __launch_bounds__(256) void k_gemv_w(QArgs a, uint32_t sb, const XT* 
     wo[j] = F::woff(a, uu[j]);
     so[j] = F::soff(a, uu[j]);
   }
-  const int stride = (int)gridDim.x * R;
-  const int n0 = (int)blockIdx.x * R + slot;
+  const int stride = gx * R;
+  const int n0 = bx * R + slot;
   uint32_t rw = (uint32_t)n0 * rb, rs = (uint32_t)n0 * sb;   // row offsets of ring slot 0
   const uint32_t dw = (uint32_t)stride * rb, ds = (uint32_t)stride * sb;
   typename F::Raw ring[D][UPT];
@@ -261,7 +270,7 @@ __global__ __launch_bounds__(256) void k_gemv_w(QArgs a, uint32_t sb, const XT* 
 #pragma unroll
   for (int j = 0; j < UPT; ++j) load_x_unit<F, XT>(xm, uu[j], xr[j], xg[j]);
 
-  for (int base = (int)blockIdx.x * R; base < N; base += D * stride) {
+  for (int base = bx * R; base < N; base += D * stride) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       const int nb = base + d * stride;      // uniform across the workgroup
@@ -1029,35 +1038,75 @@ struct GemvDot2Run {
 template <class F>
 struct GemvWaveRun {
   template <int UPT, int D, typename YT>
-  static hipError_t go(const QArgs& a, uint32_t sb, const void* x, void* y, int64_t ldy, int64_t M,
-                       int64_t N, int lshift, int grid_cap, hipStream_t st) {
+  static hipError_t go(const WaveBatch& b, uint32_t sb, const void* x, int64_t M, int lshift, int grid_cap,
+                       hipStream_t st) {
+    if (b.n == 1) return go_n<UPT, D, YT, 1>(b, sb, x, M, lshift, grid_cap, st);   // small arguments
+    return go_n<UPT, D, YT, kMaxBatch>(b, sb, x, M, lshift, grid_cap, st);
+  }
+  template <int UPT, int D, typename YT, int NB>
+  static hipError_t go_n(const WaveBatch& b, uint32_t sb, const void* x, int64_t M, int lshift, int grid_cap,
+                         hipStream_t st) {
+    // workgroups per matrix: one per R rows while the total fits the cap, else a
+    // share of the cap proportional to the rows (at least one each)
     const int R = 256 >> lshift;
-    int64_t grid = (N + R - 1) / R;
     const int64_t cap = grid_cap > 0 ? grid_cap : 1024;
-    if (grid > cap) grid = cap;
-    hipLaunchKernelGGL((k_gemv_w<F, UPT, D, f16, YT>), dim3((unsigned)grid, (unsigned)M), dim3(256), 0, st,
-                       a, sb, (const f16*)x, (YT*)y, ldy, (int)N, lshift);
+    int64_t want = 0, rows = 0;
+    for (int i = 0; i < b.n; ++i) { want += (b.N[i] + R - 1) / R; rows += b.N[i]; }
+    WaveBatchT<NB> bt{};
+    bt.n = b.n;
+    int acc = 0;
+    for (int i = 0; i < b.n; ++i) {
+      bt.a[i] = b.a[i];
+      bt.y[i] = b.y[i];
+      bt.ldy[i] = b.ldy[i];
+      bt.N[i] = b.N[i];
+      bt.b0[i] = acc;
+      int64_t g = (b.N[i] + R - 1) / R;
+      if (want > cap) {
+        const int64_t share = cap * b.N[i] / (rows > 0 ? rows : 1);
+        g = share < 1 ? 1 : share < g ? share : g;
+      }
+      acc += (int)g;
+    }
+    bt.b0[b.n] = acc;
+    hipLaunchKernelGGL((k_gemv_w<F, UPT, D, f16, YT, NB>), dim3((unsigned)acc, (unsigned)M), dim3(256), 0, st,
+                       bt, sb, (const f16*)x, lshift);
     return hipGetLastError();
   }
   template <int UPT, typename YT>
-  static hipError_t pick_d(int depth, const QArgs& a, uint32_t sb, const void* x, void* y, int64_t ldy,
-                           int64_t M, int64_t N, int lshift, int cap, hipStream_t st) {
-    if (depth == 1) return go<UPT, 1, YT>(a, sb, x, y, ldy, M, N, lshift, cap, st);
-    return go<UPT, 2, YT>(a, sb, x, y, ldy, M, N, lshift, cap, st);
+  static hipError_t pick_d(int depth, const WaveBatch& b, uint32_t sb, const void* x, int64_t M, int lshift,
+                           int cap, hipStream_t st) {
+    if (depth == 1) return go<UPT, 1, YT>(b, sb, x, M, lshift, cap, st);
+    return go<UPT, 2, YT>(b, sb, x, M, lshift, cap, st);
   }
   template <typename YT>
-  static hipError_t pick(int upt, int depth, const QArgs& a, uint32_t sb, const void* x, void* y,
-                         int64_t ldy, int64_t M, int64_t N, int lshift, int cap, hipStream_t st) {
+  static hipError_t pick(int upt, int depth, const WaveBatch& b, uint32_t sb, const void* x, int64_t M,
+                         int lshift, int cap, hipStream_t st) {
     switch (upt) {
-      case 1: return pick_d<1, YT>(depth, a, sb, x, y, ldy, M, N, lshift, cap, st);
-      case 2: return pick_d<2, YT>(depth, a, sb, x, y, ldy, M, N, lshift, cap, st);
-      case 3: return pick_d<3, YT>(depth, a, sb, x, y, ldy, M, N, lshift, cap, st);
-      default: return pick_d<4, YT>(depth, a, sb, x, y, ldy, M, N, lshift, cap, st);
+      case 1: return pick_d<1, YT>(depth, b, sb, x, M, lshift, cap, st);
+      case 2: return pick_d<2, YT>(depth, b, sb, x, M, lshift, cap, st);
+      case 3: return pick_d<3, YT>(depth, b, sb, x, M, lshift, cap, st);
+      default: return pick_d<4, YT>(depth, b, sb, x, M, lshift, cap, st);
     }
   }
+  // one matrix: a batch of one
   static hipError_t run(const QArgs& a, uint32_t sb, const void* x, bool x_f32, void* y, int64_t ldy,
                         bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st) {
+    WaveBatch b{};
+    b.n = 1;
+    b.a[0] = a;
+    b.y[0] = y;
+    b.ldy[0] = ldy;
+    b.N[0] = (int)N;
+    return run_batch(b, sb, x, x_f32, y_f32, M, o, st);
+  }
+  // b.n matrices sharing K, the format and x; b.b0 is filled here
+  static hipError_t run_batch(const WaveBatch& b, uint32_t sb, const void* x, bool x_f32, bool y_f32, int64_t M,
+                              const Opts& o, hipStream_t st) {
     if (x_f32) return hipErrorNotSupported;         // fp32 activations: ring kernel
+    const QArgs& a = b.a[0];
+    int64_t N = 0;
+    for (int i = 0; i < b.n; ++i) N += b.N[i];
     const int U = a.K / F::UE;
     int lshift;
     if (o.lanes_per_row == 16 || o.lanes_per_row == 32 || o.lanes_per_row == 64)
@@ -1074,18 +1123,41 @@ struct GemvWaveRun {
     // fast as a two-row register ring on every decode shape
     const int depth = o.depth == 2 ? 2 : 1;
     const int cap = o.grid_cap > 0 ? o.grid_cap : (N > 32768 ? 1024 : 512);
-    return y_f32 ? pick<float>(upt, depth, a, sb, x, y, ldy, M, N, lshift, cap, st)
-                 : pick<f16>(upt, depth, a, sb, x, y, ldy, M, N, lshift, cap, st);
+    return y_f32 ? pick<float>(upt, depth, b, sb, x, M, lshift, cap, st)
+                 : pick<f16>(upt, depth, b, sb, x, M, lshift, cap, st);
   }
 };
+
+template <class F>
+struct GemvWaveBatchRun {
+  static hipError_t run(const WaveBatch& b, uint32_t sb, const void* x, bool x_f32, bool y_f32, const Opts& o,
+                        hipStream_t st) {
+    return GemvWaveRun<F>::run_batch(b, sb, x, x_f32, y_f32, 1, o, st);
+  }
+};
+
+// bytes per row of the scale / bias buffers the wave kernel views (MLX, split layouts)
+static uint32_t scale_row_bytes(int fmt, const QArgs& a) {
+  return fmt == F_MLX ? (uint32_t)(2 * (a.K / a.gs)) : (fmt == F_Q8_0S || fmt == F_Q5_0S) ? (uint32_t)(2 * (a.K / 32)) : 0u;
+}
+
+hipError_t launch_gemv_batched(int fmt, const WaveBatch& b, const void* x, bool x_f32, bool y_f32, const Opts& o,
+                               hipStream_t st) {
+  if (b.n < 1 || b.n > kMaxBatch) return hipErrorNotSupported;
+  const uint32_t sb = scale_row_bytes(fmt, b.a[0]);
+  for (int i = 0; i < b.n; ++i) {               // 32-bit buffer offsets within each matrix
+    const int64_t rowb = b.a[i].rb > (int64_t)sb ? b.a[i].rb : (int64_t)sb;
+    if ((int64_t)(b.N[i] + 1024) * rowb >= ((int64_t)1 << 31) || b.N[i] <= 0) return hipErrorNotSupported;
+  }
+  return by_fmt<GemvWaveBatchRun>(fmt, b, sb, x, x_f32, y_f32, o, st);
+}
 
 hipError_t launch_gemv_dot2(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
                             bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;
   if (o.variant == 0 || o.variant == 3) {
     // scale-row bytes (MLX scales/biases, split-layout scales) for the buffer views
-    const uint32_t sb = fmt == F_MLX ? (uint32_t)(2 * (a.K / a.gs))
-                      : (fmt == F_Q8_0S || fmt == F_Q5_0S) ? (uint32_t)(2 * (a.K / 32)) : 0u;
+    const uint32_t sb = scale_row_bytes(fmt, a);
     // 32-bit buffer offsets: split the rows into ranges below 2 GiB of weights
     const int64_t wrow = a.rb > 0 ? a.rb : 1;
     const int64_t rows = ((int64_t)1 << 31) / (wrow > (int64_t)sb ? wrow : (int64_t)sb) - 1024;

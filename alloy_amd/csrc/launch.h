@@ -24,6 +24,25 @@ struct Opts {
   int variant = 0;         // dot2 GEMV: 0 automatic, 1 register ring, 2 LDS-staged tiles
 };
 
+// Several weight matrices (same format and K) against one x in a single launch:
+// each workgroup serves one matrix (block ranges b0[i] .. b0[i+1]).
+constexpr int kMaxBatch = 8;
+template <int NB>
+struct WaveBatchT {
+  int n;
+  int b0[NB + 1];
+  QArgs a[NB];
+  void* y[NB];
+  int64_t ldy[NB];
+  int N[NB];
+};
+using WaveBatch = WaveBatchT<kMaxBatch>;
+
+// M = 1 GEMV over b.n matrices in one launch (wave-row kernel);
+// hipErrorNotSupported when that kernel does not take the shape.
+hipError_t launch_gemv_batched(int fmt, const WaveBatch& b, const void* x, bool x_f32, bool y_f32,
+                               const Opts& o, hipStream_t st);
+
 hipError_t launch_dequant(int fmt, const QArgs& a, void* out, bool out_f16, int64_t row0,
                           int64_t nrows, hipStream_t st);
 hipError_t launch_gemv_dot2(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,

@@ -452,22 +452,55 @@ for _name, _fn in _SINGLE.items():
     torch.library.impl(_LIB, _name, "Meta")(_meta)
 
 
-def _batched(single):
+def _ptr_array(tensors):
+    arr = (ctypes.c_void_p * len(tensors))(*[t.data_ptr() if t is not None else None for t in tensors])
+    return arr, ctypes.cast(arr, ctypes.c_void_p)
+
+
+def _batched(name: str, single: str, fmt: str, slots: tuple):
+    """Native batched op: every matrix against the same activations in as few launches
+    as the library can (one per 8 matrices at M = 1), outputs separate (M, N_i)."""
     def run(activations, *lists):
-        return [single(activations, *bufs) for bufs in zip(*lists)]
+        mats = list(zip(*lists))
+        if not mats:
+            return []
+        M, K = _check_act(activations)
+        Ns = [_SHAPE[single](activations, *bufs) for bufs in mats]
+        gs = shape_mlx(activations, *mats[0])[3] if fmt == "mlx_q4" else 0
+        if fmt == "mlx_q4" and any(shape_mlx(activations, *b)[3] != gs for b in mats):
+            raise ValueError(f"{name}: all matrices must share one group size")
+        dev = _same_device(activations, *[b for bufs in mats for b in bufs])
+        x = activations.contiguous()
+        outs = [torch.empty((M, N), dtype=x.dtype, device=dev) for N in Ns]
+        if M == 0:
+            return outs
+        cols = {k: [None] * len(mats) for k in ("w", "aux", "scales", "biases")}
+        for i, bufs in enumerate(mats):
+            for slot, b in zip(slots, bufs):
+                cols[slot][i] = b.contiguous()
+        keep = [_ptr_array(cols[k]) if any(t is not None for t in cols[k]) else (None, None)
+                for k in ("w", "aux", "scales", "biases")]
+        y_arr = _ptr_array(outs)
+        n_arr = (ctypes.c_int64 * len(Ns))(*Ns)
+        with torch.cuda.device(dev):
+            _lib.call("alloy_qmm_batched", _lib.FMT[fmt], len(mats), *[p for _, p in keep],
+                      ctypes.cast(n_arr, ctypes.c_void_p), gs, _p(x), _dt(x.dtype, "activations"), y_arr[1],
+                      _dt(x.dtype, "output"), M, K, _stream(dev))
+        del cols, keep, y_arr, n_arr
+        return outs
     return run
 
 
 _BATCHED = {
-    "batched_gguf_q4_k_mm": "gguf_q4_k_mm",
-    "batched_gguf_q6_k_mm": "gguf_q6_k_mm",
-    "batched_gguf_q8_0_mm": "gguf_q8_0_mm",
-    "batched_gguf_q5_0_mm": "gguf_q5_0_mm",
-    "batched_mlx_q4_mm": "mlx_q4_mm",
+    "batched_gguf_q4_k_mm": ("gguf_q4_k_mm", "q4_k", ("w",)),
+    "batched_gguf_q6_k_mm": ("gguf_q6_k_mm", "q6_k", ("w",)),
+    "batched_gguf_q8_0_mm": ("gguf_q8_0_mm", "q8_0_split", ("w", "scales")),
+    "batched_gguf_q5_0_mm": ("gguf_q5_0_mm", "q5_0_split", ("w", "aux", "scales")),
+    "batched_mlx_q4_mm": ("mlx_q4_mm", "mlx_q4", ("w", "scales", "biases")),
 }
 
-for _name, _single in _BATCHED.items():
-    torch.library.impl(_LIB, _name, "CUDA")(_batched(_SINGLE[_single]))
+for _name, (_single, _fmt, _slots) in _BATCHED.items():
+    torch.library.impl(_LIB, _name, "CUDA")(_batched(_name, _single, _fmt, _slots))
 
     def _bmeta(activations, *lists, _s=_single):
         return [_empty_out(activations, _SHAPE[_s](activations, *bufs)) for bufs in zip(*lists)]

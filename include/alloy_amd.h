@@ -173,6 +173,22 @@ alloy_status alloy_mlx_moe_routed(const void* hidden, const float* router_logits
                                   float* y, void* stream);
 
 /*
+ * Batched projections: n weight matrices of one format and K against the same
+ * activations, y[i][M, N[i]] = x dequant(w[i])^T — the reference's batched_*_mm ops
+ * (custom_ops.py:50-52, 75-78, 92-95, 100-102, 105-106; handler
+ * packages/alloy-torch/src/alloy_torch/ops/linalg.py:555-682, which row-concatenates
+ * the weights into one matrix).  Here nothing is copied: for M = 1 one launch per
+ * group of up to 8 matrices serves all of them (each workgroup reads one matrix);
+ * otherwise each matrix runs as alloy_qmm.  Host arrays of n device pointers
+ * (aux / scales / biases arrays may be NULL when the format has none); outputs are
+ * separate contiguous [M, N[i]] buffers.
+ */
+alloy_status alloy_qmm_batched(alloy_format fmt, int32_t n, const void* const* w, const void* const* aux,
+                               const void* const* scales, const void* const* biases, const int64_t* N,
+                               int32_t group_size, const void* x, alloy_dtype x_dtype, void* const* y,
+                               alloy_dtype y_dtype, int64_t M, int64_t K, void* stream);
+
+/*
  * Fused gated pair y[M,N] = act(x G^T) * (x U^T) over two weight matrices of one
  * format (each passed like alloy_qmm's w / aux / scales / biases) — the reference's
  * *_silu / *_gelu ops (custom_ops.py:53-58, 79-82, 108-111; kernels

@@ -50,6 +50,16 @@ class Weight:
     def kw(self):
         return dict(scales=self.scales, biases=self.biases, aux=self.aux, group_size=self.gs)
 
+    def op_args(self):
+        """The buffers in the order of the reference op's schema."""
+        if self.fmt == "mlx_q4":
+            return [self.w, self.scales, self.biases]
+        if self.fmt == "q8_0_split":
+            return [self.w, self.scales]
+        if self.fmt == "q5_0_split":
+            return [self.w, self.aux, self.scales]
+        return [self.w]
+
     def qmm(self, x, **kw):
         return alloy_amd.qmm(self.fmt, x, self.w, N=self.N, **self.kw(), **kw)
 
@@ -212,3 +222,42 @@ def test_gemv_xs_mlx_group_sizes(dev, gs):
     for variant in (0, 7):
         y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=variant << 36).cpu().numpy()
         check(y, x, wt.W, f"mlx_q4 gs={gs} gemv_mfma M={M} variant={variant}")
+
+
+@pytest.mark.parametrize("fmt", ["q4_k", "q6_k", "q8_0_split", "q5_0_split", "mlx_q4"])
+@pytest.mark.parametrize("M", [1, 3])
+def test_batched_ops(dev, fmt, M):
+    # the reference's batched_*_mm: separate outputs per matrix; at M = 1 one launch
+    # per 8 matrices (10 matrices here: two launches), an empty matrix in between
+    rng = np.random.default_rng(40 + M)
+    K = 1024
+    Ns = [96, 33, 0, 200, 17, 64, 48, 31, 16, 130]
+    ws = [Weight(fmt, N, K, rng, dev) if N else None for N in Ns]
+    x = synth.numpy_x(M, K, rng)
+    xt = torch.from_numpy(x).to(dev)
+    name = {"q4_k": "batched_gguf_q4_k_mm", "q6_k": "batched_gguf_q6_k_mm", "q8_0_split": "batched_gguf_q8_0_mm",
+            "q5_0_split": "batched_gguf_q5_0_mm", "mlx_q4": "batched_mlx_q4_mm"}[fmt]
+    lists = None
+    for N, w in zip(Ns, ws):
+        if w is None:
+            if fmt == "mlx_q4":
+                bufs = [torch.zeros((0, K // 2), dtype=torch.uint8, device=dev),
+                        torch.zeros((0, K // 64), dtype=torch.float16, device=dev),
+                        torch.zeros((0, K // 64), dtype=torch.float16, device=dev)]
+            elif fmt == "q8_0_split":
+                bufs = [torch.zeros((0, K), dtype=torch.int8, device=dev),
+                        torch.zeros((0, K // 32), dtype=torch.float16, device=dev)]
+            elif fmt == "q5_0_split":
+                bufs = [torch.zeros((0, K // 2), dtype=torch.uint8, device=dev)] * 2 + \
+                       [torch.zeros((0, K // 32), dtype=torch.float16, device=dev)]
+            else:
+                bufs = [torch.zeros((0, K // 256 * (144 if fmt == "q4_k" else 210)), dtype=torch.uint8, device=dev)]
+        else:
+            bufs = w.op_args()
+        lists = [[b] for b in bufs] if lists is None else [l + [b] for l, b in zip(lists, bufs)]
+    outs = getattr(torch.ops.alloy, name)(xt, *lists)
+    assert len(outs) == len(Ns)
+    for N, w, y in zip(Ns, ws, outs):
+        assert y.shape == (M, N) and y.dtype == torch.float16
+        if w is not None:
+            check(y.float().cpu().numpy(), x, w.W, f"{name} M={M} N={N}")
