@@ -1473,23 +1473,35 @@ hipError_t launch_glu_combine(int act, const float* g, const float* u, void* y, 
   return hipGetLastError();
 }
 
+// Default kernel choice for 2 <= M <= 16 (measured on the config 2 / 3 shapes):
+//   Q4_K  tall (N >= 32768) and 3 <= M <= 6: 4x4x4 broadcast kernel; K > 4096: the
+//         Q4_K x-stationary kernel (its 16-slot waves beat the generic ones); else
+//         the generic x-stationary kernel
+//   Q6_K  generic x-stationary while N <= 8192, else the 16x16x32 kernel
+//   MLX   generic x-stationary
+//   other formats (and shapes the above do not take): 16x16x32 kernel
+static int mfma_variant(int fmt, int64_t M, int64_t N, int64_t K) {
+  if (fmt == F_Q4_K) {
+    if (N >= 32768 && M >= 3 && M <= 6) return 5;
+    return K > 4096 ? 6 : 7;
+  }
+  if (fmt == F_Q6_K) return N <= 8192 ? 7 : 1;
+  if (fmt == F_MLX) return 7;
+  return 1;
+}
+
 hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
                             bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;
-  if (o.variant == 7 || (o.variant == 0 && fmt == F_MLX)) {
-    const hipError_t e = launch_gemv_xs(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
-    if (e != hipErrorNotSupported) return e;
-    (void)hipGetLastError();
-  }
-  // Q4_K: x-stationary 16x16x32 kernel, except that very tall matrices with up to 8
-  // tokens run faster on the 4x4x4 broadcast kernel (fewer VGPRs, more waves)
-  if (fmt == F_Q4_K && (o.variant == 6 || (o.variant == 0 && !(N >= 32768 && M <= 8)))) {
-    const hipError_t e = launch_gemv_xs_q4k(a, x, x_f32, y, y_f32, M, N, o, st);
-    if (e != hipErrorNotSupported) return e;
-    (void)hipGetLastError();
-  }
-  if (fmt == F_Q4_K && (o.variant == 0 || o.variant == 5)) {
-    const hipError_t e = launch_gemv_q4k_m4(a, x, x_f32, y, y_f32, M, N, o, st);
+  const int v = o.variant ? o.variant : mfma_variant(fmt, M, N, a.K);
+  hipError_t e = hipErrorNotSupported;
+  if (v == 7) e = launch_gemv_xs(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
+  else if (v == 6 && fmt == F_Q4_K) e = launch_gemv_xs_q4k(a, x, x_f32, y, y_f32, M, N, o, st);
+  else if (v == 5 && fmt == F_Q4_K) e = launch_gemv_q4k_m4(a, x, x_f32, y, y_f32, M, N, o, st);
+  if (e != hipErrorNotSupported) return e;
+  (void)hipGetLastError();
+  if (fmt == F_Q4_K && o.variant == 0 && v != 6) {     // e.g. K over 8192 for the generic kernel
+    e = launch_gemv_xs_q4k(a, x, x_f32, y, y_f32, M, N, o, st);
     if (e != hipErrorNotSupported) return e;
     (void)hipGetLastError();
   }
