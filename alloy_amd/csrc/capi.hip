@@ -248,6 +248,21 @@ alloy_status alloy_mlx_moe_routed(const void* hidden, const float* logits, const
   return hip_status(alloy::launch_mlx_moe(m, L, (hipStream_t)stream), "moe launch");
 }
 
+alloy_status alloy_embedding(alloy_format fmt, const void* w, const void* aux, const void* scales,
+                             const void* biases, int32_t group_size, const void* ids, int32_t ids_int64,
+                             int64_t n_ids, int64_t N, int64_t K, float* out, void* stream) {
+  QArgs a;
+  alloy_status s = make_args((int)fmt, w, aux, scales, biases, group_size, K, a);
+  if (s != ALLOY_OK) return s;
+  if (n_ids < 0 || N < 0) return fail(ALLOY_E_SHAPE, "negative n_ids=%lld or N=%lld", (long long)n_ids, (long long)N);
+  if (n_ids == 0) return ALLOY_OK;
+  if (!ids || !out) return fail(ALLOY_E_ARG, "null ids or output pointer");
+  if (!aligned(ids, ids_int64 ? 8 : 4)) return fail(ALLOY_E_ALIGN, "ids misaligned");
+  if (!aligned(out, 16)) return fail(ALLOY_E_ALIGN, "output not 16-byte aligned");
+  return hip_status(alloy::launch_embedding((int)fmt, a, ids, ids_int64 != 0, n_ids, N, out, (hipStream_t)stream),
+                    "embedding launch");
+}
+
 alloy_status alloy_qmm_batched(alloy_format fmt, int32_t n, const void* const* w, const void* const* aux,
                                const void* const* scales, const void* const* biases, const int64_t* N,
                                int32_t group_size, const void* x, alloy_dtype x_dtype, void* const* y,

@@ -70,6 +70,42 @@ __global__ __launch_bounds__(256) void k_dequant(QArgs a, void* out, int out_f16
   }
 }
 
+// ------------------------------------------------------------------ quantized embedding
+// One thread per (id, 32-element group): out[i, :] = exact fp32 decode of row ids[i];
+// ids outside [0, N) give zero rows (no weight bytes are read for them).
+template <class F>
+__global__ __launch_bounds__(256) void k_embed(QArgs a, const void* ids, int ids64, int64_t n_ids, int64_t N,
+                                               float* out) {
+  const int64_t groups = a.K >> 5;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_ids * groups) return;
+  const int64_t i = t / groups;
+  const int k0 = (int)(t - i * groups) * 32;
+  const int64_t id = ids64 ? ((const int64_t*)ids)[i] : (int64_t)((const int32_t*)ids)[i];
+  float w[32];
+  if (id >= 0 && id < N) {
+    F::dec32(a, id, k0, w);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 32; ++e) w[e] = 0.f;
+  }
+  float* p = out + i * a.K + k0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) *(f32x4*)(p + 4 * j) = f32x4{w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]};
+}
+
+template <class F>
+struct EmbedRun {
+  static hipError_t run(const QArgs& a, const void* ids, bool ids64, int64_t n_ids, int64_t N, float* out,
+                        hipStream_t st) {
+    const int64_t work = n_ids * (a.K >> 5);
+    if (work == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_embed<F>, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, st, a, ids, (int)ids64, n_ids,
+                       N, out);
+    return hipGetLastError();
+  }
+};
+
 // ------------------------------------------------------------------ M=1 GEMV (v_dot2)
 // Each thread owns UPT decode units of the row (the same units for every row it
 // visits) and keeps their x values in registers: fp16 pairs in the format's XPERM
@@ -954,6 +990,11 @@ struct DequantRun {
 hipError_t launch_dequant(int fmt, const QArgs& a, void* out, bool out_f16, int64_t row0,
                           int64_t nrows, hipStream_t st) {
   return by_fmt<DequantRun>(fmt, a, out, out_f16, row0, nrows, st);
+}
+
+hipError_t launch_embedding(int fmt, const QArgs& a, const void* ids, bool ids64, int64_t n_ids, int64_t N,
+                            float* out, hipStream_t st) {
+  return by_fmt<EmbedRun>(fmt, a, ids, ids64, n_ids, N, out, st);
 }
 
 static int pow2_floor(int v) {

@@ -43,6 +43,10 @@ using WaveBatch = WaveBatchT<kMaxBatch>;
 hipError_t launch_gemv_batched(int fmt, const WaveBatch& b, const void* x, bool x_f32, bool y_f32,
                                const Opts& o, hipStream_t st);
 
+// Rows ids[0..n_ids) of an N-row matrix decoded to fp32 (ids outside [0, N): zeros).
+hipError_t launch_embedding(int fmt, const QArgs& a, const void* ids, bool ids64, int64_t n_ids, int64_t N,
+                            float* out, hipStream_t st);
+
 hipError_t launch_dequant(int fmt, const QArgs& a, void* out, bool out_f16, int64_t row0,
                           int64_t nrows, hipStream_t st);
 hipError_t launch_gemv_dot2(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,

@@ -24,6 +24,14 @@ _MM = {
 }
 
 
+_EMBED = {
+    "q8_0": lambda: torch.ops.alloy.gguf_q8_0_embedding.default,
+    "q5_0": lambda: torch.ops.alloy.gguf_q5_0_embedding.default,
+    "q4_k": lambda: torch.ops.alloy.gguf_q4_k_embedding.default,
+    "q6_k": lambda: torch.ops.alloy.gguf_q6_k_embedding.default,
+}
+
+
 class GGUFQuantLinear(torch.nn.Module):
     FORMAT: QuantFormat
 
@@ -67,6 +75,87 @@ class GGUFQ4_KLinear(GGUFQuantLinear):
 class GGUFQ6_KLinear(GGUFQuantLinear):
     """Linear over GGUF Q6_K 210-byte blocks."""
     FORMAT = QUANT_FORMATS["q6_k"]
+
+
+class GGUFQuantEmbedding(torch.nn.Module):
+    """Embedding over GGUF packed weights (``S/gguf/quant.py:144-197``): ``forward(ids)``
+    returns the exact fp32 rows ``(*ids.shape, embedding_dim)`` times ``embed_scale``."""
+
+    FORMAT: QuantFormat
+
+    def __init__(self, *, num_embeddings: int, embedding_dim: int, embed_scale: float = 1.0,
+                 **buffers: torch.Tensor) -> None:
+        super().__init__()
+        validate_quant_buffers(self.FORMAT, buffers, rows=num_embeddings, dim=embedding_dim, kind="embedding")
+        self.num_embeddings = int(num_embeddings)
+        self.embedding_dim = int(embedding_dim)
+        self.embed_scale = float(embed_scale)
+        for b in self.FORMAT.buffers:
+            self.register_buffer(b.name, buffers[b.name].contiguous())
+
+    def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
+        out = _EMBED[self.FORMAT.name]()(input_ids, *(self._buffers[b.name] for b in self.FORMAT.buffers))
+        if self.embed_scale != 1.0:
+            out = out * self.embed_scale
+        return out
+
+
+class GGUFQ8_0Embedding(GGUFQuantEmbedding):
+    FORMAT = QUANT_FORMATS["q8_0"]
+
+
+class GGUFQ5_0Embedding(GGUFQuantEmbedding):
+    FORMAT = QUANT_FORMATS["q5_0"]
+
+
+class GGUFQ4_KEmbedding(GGUFQuantEmbedding):
+    FORMAT = QUANT_FORMATS["q4_k"]
+
+
+class GGUFQ6_KEmbedding(GGUFQuantEmbedding):
+    FORMAT = QUANT_FORMATS["q6_k"]
+
+
+_TIED = {GGUFQ8_0Embedding: GGUFQ8_0Linear, GGUFQ5_0Embedding: GGUFQ5_0Linear,
+         GGUFQ4_KEmbedding: GGUFQ4_KLinear, GGUFQ6_KEmbedding: GGUFQ6_KLinear}
+
+
+def tied_output_head(embedding: torch.nn.Module, output: torch.nn.Module | None = None) -> torch.nn.Module:
+    """The quantized lm_head that shares a quantized input embedding's buffers
+    (``S/gguf/quant.py:553-623``): a Linear output head without bias becomes the
+    matching GGUF Linear over the same rows; anything else raises as the reference does.
+    An ``MLXQ4Embedding`` becomes an ``MLXQ4Linear`` over its buffers
+    (``packages/alloy-server/src/alloy_server/mlx/quant.py:148-168``)."""
+    if isinstance(embedding, MLXQ4Embedding):
+        if output is not None and not isinstance(output, torch.nn.Linear):
+            raise TypeError(f"Tied MLX embeddings require a Linear output head, got {type(output).__name__}")
+        return MLXQ4Linear(in_features=embedding.embedding_dim, out_features=embedding.num_embeddings,
+                           qweight=embedding.qweight, scales=embedding.scales, biases=embedding.biases)
+    cls = _TIED.get(type(embedding))
+    if cls is None:
+        raise TypeError(f"no tied output head for {type(embedding).__name__}")
+    name = embedding.FORMAT.name.upper()
+    if output is not None and not isinstance(output, torch.nn.Linear):
+        raise TypeError(f"Tied {name} GGUF embeddings require a Linear output head, got {type(output).__name__}")
+    if output is not None and output.bias is not None:
+        raise NotImplementedError(f"Tied {name} GGUF output head bias is not supported")
+    bufs = {b.name: embedding._buffers[b.name] for b in embedding.FORMAT.buffers}
+    return cls(in_features=embedding.embedding_dim, out_features=embedding.num_embeddings, **bufs)
+
+
+class MLXQ4Embedding(torch.nn.Module):
+    """Embedding over MLX 4-bit affine weights: exact fp32 rows of ``mlx_q4_embedding``."""
+
+    def __init__(self, *, num_embeddings: int, embedding_dim: int, qweight: torch.Tensor, scales: torch.Tensor,
+                 biases: torch.Tensor) -> None:
+        super().__init__()
+        validate_mlx_buffers(qweight, scales, biases, rows=num_embeddings, dim=embedding_dim, kind="embedding")
+        self.num_embeddings, self.embedding_dim = int(num_embeddings), int(embedding_dim)
+        for name, t in (("qweight", qweight), ("scales", scales), ("biases", biases)):
+            self.register_buffer(name, t.contiguous())
+
+    def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
+        return torch.ops.alloy.mlx_q4_embedding.default(input_ids, self.qweight, self.scales, self.biases)
 
 
 class MLXQ4Linear(torch.nn.Module):

@@ -267,6 +267,67 @@ def _q8_0_silu(activations, gq, gsc, uq, usc):
     return _run_glu("alloy_gguf_q8_0_silu", "q8_0_split", activations, [gq, gsc], [uq, usc], M, N, K)
 
 
+def _embedding(fmt: str, input_ids: torch.Tensor, bufs: dict, N: int, K: int, gs: int = 0) -> torch.Tensor:
+    if input_ids.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"input_ids must be int32 or int64, got {input_ids.dtype}")
+    dev = _same_device(input_ids, *[b for b in bufs.values() if b is not None])
+    ids = input_ids.contiguous()
+    out = torch.empty(tuple(ids.shape) + (K,), dtype=torch.float32, device=dev)
+    if ids.numel():
+        with torch.cuda.device(dev):
+            _lib.call("alloy_embedding", _lib.FMT[fmt], _p(bufs.get("w")), _p(bufs.get("aux")),
+                      _p(bufs.get("scales")), _p(bufs.get("biases")), gs, _p(ids),
+                      int(ids.dtype == torch.int64), ids.numel(), N, K, _p(out), _stream(dev))
+    return out
+
+
+def _emb_rows(t: torch.Tensor, what: str) -> int:
+    if t.ndim != 2:
+        raise ValueError(f"{what} must be 2-D, got shape {tuple(t.shape)}")
+    return t.shape[0]
+
+
+def _q4_k_embedding(input_ids, blocks):
+    if blocks.dtype != torch.uint8 or blocks.ndim != 2 or blocks.shape[1] % 144:
+        raise ValueError(f"gguf_q4_k_embedding: blocks must be uint8 (N, k*144), got {tuple(blocks.shape)}")
+    return _embedding("q4_k", input_ids, dict(w=blocks.contiguous()), blocks.shape[0], blocks.shape[1] // 144 * 256)
+
+
+def _q6_k_embedding(input_ids, packed_weights):
+    if packed_weights.dtype != torch.uint8 or packed_weights.ndim != 2 or packed_weights.shape[1] % 210:
+        raise ValueError(f"gguf_q6_k_embedding: packed_weights must be uint8 (N, k*210), got {tuple(packed_weights.shape)}")
+    return _embedding("q6_k", input_ids, dict(w=packed_weights.contiguous()), packed_weights.shape[0],
+                      packed_weights.shape[1] // 210 * 256)
+
+
+def _q8_0_embedding(input_ids, qweight, scales):
+    N, K = _emb_rows(qweight, "qweight"), qweight.shape[1]
+    if qweight.dtype != torch.int8 or scales.dtype != torch.float16 or tuple(scales.shape) != (N, K // 32) or K % 32:
+        raise ValueError("gguf_q8_0_embedding: qweight int8 (N, K) and scales float16 (N, K/32) expected")
+    return _embedding("q8_0_split", input_ids, dict(w=qweight.contiguous(), scales=scales.contiguous()), N, K)
+
+
+def _q5_0_embedding(input_ids, qweight, qhigh, scales):
+    N, K = _emb_rows(qweight, "qweight"), qweight.shape[1] * 2
+    if (qweight.dtype != torch.uint8 or qhigh.dtype != torch.uint8 or tuple(qhigh.shape) != tuple(qweight.shape)
+            or scales.dtype != torch.float16 or tuple(scales.shape) != (N, K // 32) or K % 32):
+        raise ValueError("gguf_q5_0_embedding: qweight/qhigh uint8 (N, K/2) and scales float16 (N, K/32) expected")
+    return _embedding("q5_0_split", input_ids,
+                      dict(w=qweight.contiguous(), aux=qhigh.contiguous(), scales=scales.contiguous()), N, K)
+
+
+def _mlx_embedding(input_ids, qweight, scales, biases):
+    N = _emb_rows(qweight, "qweight")
+    K = qweight.shape[1] * 2
+    if scales.ndim != 2 or scales.shape[0] != N or tuple(biases.shape) != tuple(scales.shape):
+        raise ValueError("mlx_q4_embedding: scales/biases must be (N, K/group)")
+    gs = K // scales.shape[1] if scales.shape[1] else 0
+    if gs <= 0 or gs * scales.shape[1] != K:
+        raise ValueError(f"mlx_q4_embedding: group size does not divide K={K}")
+    return _embedding("mlx_q4", input_ids, dict(w=qweight.contiguous(), scales=scales.contiguous(),
+                                                  biases=biases.contiguous()), N, K, gs)
+
+
 def gguf_moe_routed(hidden, router_logits, gate_up_blocks, down_qweight, num_experts: int, top_k: int,
                     moe_intermediate: int, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Routed GGUF experts (Q4_K fused gate/up, Q6_K down) -> float32 (T, H), like the
@@ -347,6 +408,12 @@ _LIB.define("batched_mlx_q4_mm(Tensor activations, Tensor[] qweights, Tensor[] s
 # wire-block Q8_0 / Q5_0 (the raw GGUF blob; the reference only has the split ops)
 _LIB.define("gguf_q8_0_blocks_mm(Tensor activations, Tensor blocks) -> Tensor")
 _LIB.define("gguf_q5_0_blocks_mm(Tensor activations, Tensor blocks) -> Tensor")
+# quantized embeddings (reference custom_ops.py:67-69, 83-85, 89-91, 97-99, 103)
+_LIB.define("gguf_q4_k_embedding(Tensor input_ids, Tensor blocks) -> Tensor")
+_LIB.define("gguf_q6_k_embedding(Tensor input_ids, Tensor packed_weights) -> Tensor")
+_LIB.define("gguf_q8_0_embedding(Tensor input_ids, Tensor qweight, Tensor scales) -> Tensor")
+_LIB.define("gguf_q5_0_embedding(Tensor input_ids, Tensor qweight, Tensor qhigh, Tensor scales) -> Tensor")
+_LIB.define("mlx_q4_embedding(Tensor input_ids, Tensor qweight, Tensor scales, Tensor biases) -> Tensor")
 # fused gated pairs (reference custom_ops.py:53-58, 79-82, 108-111)
 _LIB.define("gguf_q4_k_silu(Tensor activations, Tensor gate_blocks, Tensor up_blocks) -> Tensor")
 _LIB.define("gguf_q4_k_gelu(Tensor activations, Tensor gate_blocks, Tensor up_blocks) -> Tensor")
@@ -510,6 +577,22 @@ for _name, (_single, _fmt, _slots) in _BATCHED.items():
 
 torch.library.impl(_LIB, "mlx_moe_routed", "CUDA")(mlx_moe_routed)
 torch.library.impl(_LIB, "gguf_moe_routed", "CUDA")(gguf_moe_routed)
+
+_EMB = {
+    "gguf_q4_k_embedding": (_q4_k_embedding, lambda ids, b: b.shape[1] // 144 * 256),
+    "gguf_q6_k_embedding": (_q6_k_embedding, lambda ids, b: b.shape[1] // 210 * 256),
+    "gguf_q8_0_embedding": (_q8_0_embedding, lambda ids, q, s: q.shape[1]),
+    "gguf_q5_0_embedding": (_q5_0_embedding, lambda ids, q, h, s: q.shape[1] * 2),
+    "mlx_q4_embedding": (_mlx_embedding, lambda ids, q, s, b: q.shape[1] * 2),
+}
+for _name, (_fn, _width) in _EMB.items():
+    torch.library.impl(_LIB, _name, "CUDA")(_fn)
+
+    def _emb_meta(input_ids, *bufs, _w=_width):
+        return torch.empty(tuple(input_ids.shape) + (_w(input_ids, *bufs),), dtype=torch.float32,
+                           device=input_ids.device)
+
+    torch.library.impl(_LIB, _name, "Meta")(_emb_meta)
 
 _GLU = {
     "gguf_q4_k_silu": (_q4_k_silu, shape_glu_q4_k),

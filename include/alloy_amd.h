@@ -173,6 +173,19 @@ alloy_status alloy_mlx_moe_routed(const void* hidden, const float* router_logits
                                   float* y, void* stream);
 
 /*
+ * Quantized embedding lookup — the reference's gguf_q4_k_embedding,
+ * gguf_q6_k_embedding, gguf_q8_0_embedding, gguf_q5_0_embedding, mlx_q4_embedding
+ * (custom_ops.py:67-69, 83-85, 89-91, 97-99, 103; kernels
+ * packages/alloy-metal/src/alloy/std/quant.py:811-884, 1165-1270, 2804-2830):
+ * out[i, :] = the exact fp32 decode of weight row ids[i] (K values), for n_ids ids
+ * (int32, or int64 when ids_int64); an id outside [0, N) gives a zero row.  The
+ * weight buffers are passed as for alloy_qmm; out is f32[n_ids, K], 16-byte aligned.
+ */
+alloy_status alloy_embedding(alloy_format fmt, const void* w, const void* aux, const void* scales,
+                             const void* biases, int32_t group_size, const void* ids, int32_t ids_int64,
+                             int64_t n_ids, int64_t N, int64_t K, float* out, void* stream);
+
+/*
  * Batched projections: n weight matrices of one format and K against the same
  * activations, y[i][M, N[i]] = x dequant(w[i])^T — the reference's batched_*_mm ops
  * (custom_ops.py:50-52, 75-78, 92-95, 100-102, 105-106; handler

@@ -261,3 +261,64 @@ def test_batched_ops(dev, fmt, M):
         assert y.shape == (M, N) and y.dtype == torch.float16
         if w is not None:
             check(y.float().cpu().numpy(), x, w.W, f"{name} M={M} N={N}")
+
+
+@pytest.mark.parametrize("fmt", ["q4_k", "q6_k", "q8_0_split", "q5_0_split", "mlx_q4"])
+def test_embedding_bit_exact(dev, fmt):
+    # the reference's gguf_q*_embedding / mlx_q4_embedding: exact fp32 rows; ids
+    # outside the table give zero rows; int32 and int64 ids, any id shape
+    rng = np.random.default_rng(23)
+    N, K = 300, 1024
+    wt = Weight(fmt, N, K, rng, dev)
+    name = {"q4_k": "gguf_q4_k_embedding", "q6_k": "gguf_q6_k_embedding", "q8_0_split": "gguf_q8_0_embedding",
+            "q5_0_split": "gguf_q5_0_embedding", "mlx_q4": "mlx_q4_embedding"}[fmt]
+    ids = rng.integers(0, N, size=(3, 7))
+    ids[0, 0], ids[2, 6] = -1, N
+    for dt in (torch.int64, torch.int32):
+        out = getattr(torch.ops.alloy, name)(torch.from_numpy(ids).to(dev).to(dt), *wt.op_args())
+        assert out.shape == (3, 7, K) and out.dtype == torch.float32
+        got = out.cpu().numpy()
+        want = np.where(((ids >= 0) & (ids < N))[..., None], wt.W[np.clip(ids, 0, N - 1)], 0.0).astype(np.float32)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"{name} {dt}"
+
+
+def test_embedding_modules_and_tied_head(dev):
+    rng = np.random.default_rng(4)
+    N, K = 64, 512
+    wt = Weight("q4_k", N, K, rng, dev)
+    emb = alloy_amd.GGUFQ4_KEmbedding(num_embeddings=N, embedding_dim=K, embed_scale=2.0, blocks=wt.w)
+    ids = torch.tensor([[1, 5, 63]], device=dev)
+    assert np.array_equal(emb(ids).cpu().numpy()[0], 2.0 * wt.W[[1, 5, 63]])
+    head = alloy_amd.tied_output_head(emb, torch.nn.Linear(K, N, bias=False))
+    x = torch.from_numpy(synth.numpy_x(2, K, rng)).to(dev)
+    check(head(x).float().cpu().numpy(), x.cpu().numpy(), wt.W, "tied Q4_K head")
+    with pytest.raises(NotImplementedError):
+        alloy_amd.tied_output_head(emb, torch.nn.Linear(K, N, bias=True))
+
+
+@pytest.mark.gpu
+def test_modules_loaded_from_gguf_and_mlx_files(dev, tmp_path):
+    """GGUF file -> GGUF*Linear / Embedding and MLX safetensors -> MLXQ4Linear on the GPU."""
+    from safetensors.torch import save_file
+
+    from alloy_amd import gguf, mlx
+    rng = np.random.default_rng(21)
+    N, K = 96, 1024
+    blobs = {fm: synth.numpy_blocks(fm, N, K, rng) for fm in ("q8_0", "q5_0", "q4_k", "q6_k")}
+    p = tmp_path / "w.gguf"
+    gguf.write_gguf(p, {"general.architecture": "llama"}, [(f"w.{fm}", fm, (K, N), b) for fm, b in blobs.items()])
+    f = gguf.read_gguf(p)
+    x = torch.from_numpy(synth.numpy_x(3, K, rng)).to(dev)
+    for fm, b in blobs.items():
+        W = oq.dequant(fm, b, K)
+        check(f.linear(f"w.{fm}").to(dev)(x).float().cpu().numpy(), x.cpu().numpy(), W, f"gguf file {fm}")
+        emb = f.embedding(f"w.{fm}").to(dev)
+        ids = torch.tensor([0, 7, N - 1], device=dev)
+        assert np.array_equal(emb(ids).cpu().numpy(), W[[0, 7, N - 1]]), fm
+    q8, s, bb = synth.numpy_mlx(N, K, 64, rng)
+    st = tmp_path / "model.safetensors"
+    save_file({"proj.weight": torch.from_numpy(q8.view("<u4").copy()).view(torch.int32),
+               "proj.scales": torch.from_numpy(s), "proj.biases": torch.from_numpy(bb)}, str(st))
+    ck = mlx.read_mlx_checkpoint([st], {"quantization": {"group_size": 64, "bits": 4}})
+    W = oq.dequant("mlx_q4", q8, K, scales=s, biases=bb, group_size=64)
+    check(ck.linear("proj").to(dev)(x).float().cpu().numpy(), x.cpu().numpy(), W, "mlx file")

@@ -165,3 +165,19 @@ def test_gguf_moe_modules_validate_like_reference():
         GGUFQwen35MoeExperts(gate_up_blocks=torch.zeros((E, 2 * I, 288), dtype=torch.int8),
                              down_qweight=torch.zeros((E, H, 210), dtype=torch.uint8), num_experts=E,
                              hidden_size=H, moe_intermediate_size=I)
+
+
+def test_embedding_meta_and_modules():
+    ids = meta((2, 3), torch.int64)
+    assert torch.ops.alloy.gguf_q6_k_embedding(ids, meta((10, 420), torch.uint8)).shape == (2, 3, 512)
+    assert torch.ops.alloy.gguf_q8_0_embedding(ids, meta((10, 64), torch.int8), meta((10, 2), torch.float16)).shape == (2, 3, 64)
+    assert torch.ops.alloy.gguf_q5_0_embedding(ids, meta((10, 32), torch.uint8), meta((10, 32), torch.uint8),
+                                               meta((10, 2), torch.float16)).shape == (2, 3, 64)
+    from alloy_amd.modules import GGUFQ6_KEmbedding, tied_output_head
+    e = GGUFQ6_KEmbedding(num_embeddings=4, embedding_dim=256, qweight=torch.zeros((4, 210), dtype=torch.uint8))
+    head = tied_output_head(e)
+    assert head.out_features == 4 and head.in_features == 256 and head.qweight.data_ptr() == e.qweight.data_ptr()
+    with pytest.raises(TypeError):
+        tied_output_head(e, torch.nn.Embedding(4, 256))
+    with pytest.raises(ValueError):
+        GGUFQ6_KEmbedding(num_embeddings=4, embedding_dim=100, qweight=torch.zeros((4, 210), dtype=torch.uint8))
