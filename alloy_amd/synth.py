@@ -1,6 +1,6 @@
 """Seeded synthetic weights/activations with the distributions of the benchmark configs.
 
-Distributions (one per format):
+Distributions (one per format, as the benchmark configurations state them):
   Q8_0   d = fp16(|N(0,1)|*0.01), q ~ U{-127..127} int8
   Q4_K   d, dmin = fp16(|N(0,1)|*0.005), 12 scale bytes + 128 quant bytes ~ U{0..255}
   Q6_K   ql, qh ~ U{0..255}, scales ~ U{-64..63} int8, d = fp16(|N(0,1)|*0.002)
