@@ -3,29 +3,13 @@
 // HIP stream; no allocation, no global mutable state.
 #include <type_traits>
 
+#include "gemv.h"
 #include "launch.h"
 #include "xs.h"
 
 namespace alloy {
 
 // ------------------------------------------------------------------ helpers
-template <typename XT>
-__device__ __forceinline__ f16x8 ld_x8(const XT* p);
-template <>
-__device__ __forceinline__ f16x8 ld_x8<f16>(const f16* p) { return *(const f16x8*)p; }
-template <>
-__device__ __forceinline__ f16x8 ld_x8<float>(const float* p) {
-  const f32x4 a = *(const f32x4*)p, b = *(const f32x4*)(p + 4);
-  f16x8 r;
-  r[0] = (f16)a[0]; r[1] = (f16)a[1]; r[2] = (f16)a[2]; r[3] = (f16)a[3];
-  r[4] = (f16)b[0]; r[5] = (f16)b[1]; r[6] = (f16)b[2]; r[7] = (f16)b[3];
-  return r;
-}
-
-__device__ __forceinline__ uint32_t pack2(f16 lo, f16 hi) {
-  return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
-}
-
 __device__ __forceinline__ void store_y(void* y, bool y_f32, int64_t i, float v) {
   if (y_f32) ((float*)y)[i] = v;
   else ((f16*)y)[i] = (f16)v;
@@ -114,49 +98,6 @@ struct EmbedRun {
 // its rows with a grid stride; the next row's weight bytes are loaded while the
 // current row is computed.  Row sums are reduced in a fixed order (shuffles inside
 // a wave, then LDS across waves).  grid.y = activation row.
-template <class F, typename XT>
-__device__ __forceinline__ void load_x_unit(const XT* x, int u, uint32_t (&xr)[F::UE / 2],
-                                            float (&xg)[F::UE / 16]) {
-  constexpr int RUN = F::RUN;
-#pragma unroll
-  for (int r = 0; r < F::UE / RUN; ++r) {
-    const XT* p = x + F::run_start(u, r);
-    f16 v[RUN];
-#pragma unroll
-    for (int c = 0; c < RUN / 8; ++c) {
-      const f16x8 t = ld_x8<XT>(p + 8 * c);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[8 * c + e] = t[e];
-    }
-    uint32_t* o = xr + (RUN / 2) * r;
-    if (F::XPERM == 4) {
-#pragma unroll
-      for (int j = 0; j < RUN / 4; ++j) {
-        o[2 * j] = pack2(v[4 * j], v[4 * j + 2]);
-        o[2 * j + 1] = pack2(v[4 * j + 1], v[4 * j + 3]);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < RUN / 8; ++j) {
-        const int b = 8 * j;
-        o[4 * j] = pack2(v[b], v[b + 4]);
-        o[4 * j + 1] = pack2(v[b + 2], v[b + 6]);
-        o[4 * j + 2] = pack2(v[b + 1], v[b + 5]);
-        o[4 * j + 3] = pack2(v[b + 3], v[b + 7]);
-      }
-    }
-    // per-16-element sums: pairs 8h..8h+7 hold exactly elements 16h..16h+15 in
-    // either order; v_dot2 against (1, 1) adds them in fp32 without conversions
-#pragma unroll
-    for (int h = 0; h < RUN / 16; ++h) {
-      float sum = 0.f;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) sum = dot2(o[8 * h + q], MAGIC1, sum);
-      xg[(RUN / 16) * r + h] = sum;
-    }
-  }
-}
-
 template <class F, int UPT, int D, typename XT>
 __global__ __launch_bounds__(256) void k_gemv_dot2(QArgs a, const XT* x, void* y, int y_f32,
                                                    int64_t N, int C16) {
@@ -233,6 +174,13 @@ __global__ __launch_bounds__(256) void k_gemv_dot2(QArgs a, const XT* x, void* y
 }
 
 // ------------------------------------------------------------------ M=1 GEMV, wave rows
+// Formats whose wave-path raw loads are completed across lanes before the dot
+// (F::share), e.g. a header loaded a dword per lane.
+template <class F, class = void>
+struct HasShare : std::false_type {};
+template <class F>
+struct HasShare<F, std::void_t<decltype(F::share(std::declval<typename F::Raw&>()))>> : std::true_type {};
+
 // L = 16, 32 or 64 lanes share a row inside one wave (64/L rows per wave, 256/L per
 // workgroup); each lane owns UPT decode units of the row, the same for every row
 // it visits, with their x in registers.  Weights stream through a ring of D rows
@@ -240,22 +188,6 @@ __global__ __launch_bounds__(256) void k_gemv_dot2(QArgs a, const XT* x, void* y
 // (no clamps, no faults), so every refill is unconditional.  A row's partial sums
 // reduce across its L lanes with DPP (quad_perm, row mirrors, row_bcast 15/31) —
 // no LDS, no barrier — and the row's last lane stores it.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_f(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROW_MASK, 0xF, false));
-}
-// Sum over groups of 1 << lshift lanes (16, 32 or 64); the total is complete in the
-// group's last lane.  Branch-free in lshift, so the loop body has no control flow.
-__device__ __forceinline__ float dpp_sum_rows(float v, int lshift) {
-  v += dpp_f<0xB1, 0xF>(v);     // quad_perm [1,0,3,2]
-  v += dpp_f<0x4E, 0xF>(v);     // quad_perm [2,3,0,1]
-  v += dpp_f<0x141, 0xF>(v);    // row_half_mirror: 8-lane sums
-  v += dpp_f<0x140, 0xF>(v);    // row_mirror: every lane of a 16-lane row holds its sum
-  const float s32 = v + dpp_f<0x142, 0xA>(v);        // row_bcast:15 -> rows 1, 3: 32-lane sums
-  const float s64 = s32 + dpp_f<0x143, 0xC>(s32);    // row_bcast:31 -> row 3: 64-lane sum
-  return lshift == 4 ? v : lshift == 5 ? s32 : s64;
-}
-
 template <class F, int UPT, int D, typename XT, typename YT, int NB>
 __global__ __launch_bounds__(256) void k_gemv_w(WaveBatchT<NB> bt, uint32_t sb, const XT* x, int lshift) {
   // this workgroup's matrix: the batch entry whose block range holds blockIdx.x
@@ -287,24 +219,44 @@ __global__ __launch_bounds__(256) void k_gemv_w(WaveBatchT<NB> bt, uint32_t sb, 
   for (int j = 0; j < UPT; ++j) {
     const int u = li + L * j;
     own[j] = u < U;
-    uu[j] = own[j] ? u : U - 1;            // x and decode of a valid unit; result dropped
-    wo[j] = F::woff(a, uu[j]);
-    so[j] = F::soff(a, uu[j]);
+    uu[j] = own[j] ? u : U - 1;            // x of a valid unit; result dropped
+    // a unit past the row's end loads from past the buffer's end: zeros, no traffic
+    wo[j] = own[j] ? F::woff(a, uu[j]) : 0x80000000u;
+    so[j] = own[j] ? F::soff(a, uu[j]) : 0x80000000u;
   }
   const int stride = gx * R;
   const int n0 = bx * R + slot;
   uint32_t rw = (uint32_t)n0 * rb, rs = (uint32_t)n0 * sb;   // row offsets of ring slot 0
   const uint32_t dw = (uint32_t)stride * rb, ds = (uint32_t)stride * sb;
+  // Activation row m reaches the lanes through LDS: one coalesced copy per workgroup
+  // (global -> registers, issued before the weight ring so the wait for it leaves the
+  // ring in flight, -> LDS), then each lane reads the x of its units.  Loading x per
+  // lane from global memory instead re-reads the same few KiB for every row slot of
+  // every workgroup, which costs L1/L2 cycles comparable to the weights themselves.
+  static_assert(std::is_same<XT, f16>::value, "wave-row GEMV takes fp16 activations");
+  constexpr int XV = 512 * F::UE / 4096;          // 16-byte chunks per thread at the largest K
+  __shared__ __attribute__((aligned(16))) f16 xl[256 * F::UE];
+  const uint32_t xbytes = 2u * (uint32_t)K;
+  const __amdgpu_buffer_rsrc_t xrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(x + m * K), (short)0, (int)xbytes, ALLOY_RSRC_DW3);
+  u32x4 xv[XV];
+#pragma unroll
+  for (int i = 0; i < XV; ++i)
+    if (4096u * i < xbytes) xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (uint32_t)t * 16u + 4096u * i, 0, 0);
   typename F::Raw ring[D][UPT];
 #pragma unroll
   for (int d = 0; d < D; ++d)
 #pragma unroll
     for (int j = 0; j < UPT; ++j) ring[d][j] = F::load_b(src, rw + d * dw + wo[j], rs + d * ds + so[j], uu[j]);
+#pragma unroll
+  for (int i = 0; i < XV; ++i)
+    if (4096u * i < xbytes) *(u32x4*)((uint8_t*)xl + t * 16 + 4096 * i) = xv[i];
+  lgkm_wait0();
+  wg_barrier();
   uint32_t xr[UPT][F::UE / 2];
   float xg[UPT][F::UE / 16];
-  const XT* xm = x + m * K;
 #pragma unroll
-  for (int j = 0; j < UPT; ++j) load_x_unit<F, XT>(xm, uu[j], xr[j], xg[j]);
+  for (int j = 0; j < UPT; ++j) load_x_unit<F, f16>(xl, uu[j], xr[j], xg[j]);
 
   for (int base = bx * R; base < N; base += D * stride) {
 #pragma unroll
@@ -317,6 +269,7 @@ __global__ __launch_bounds__(256) void k_gemv_w(WaveBatchT<NB> bt, uint32_t sb, 
       float acc = 0.f;
 #pragma unroll
       for (int j = 0; j < UPT; ++j) {
+        if constexpr (HasShare<F>::value) F::share(ring[d][j]);
         const float v = F::dot(ring[d][j], uu[j], xr[j], xg[j]);
         acc += own[j] ? v : 0.f;
       }
@@ -1163,7 +1116,11 @@ struct GemvWaveRun {
     // one row in flight per lane, latency hidden by occupancy: measured at least as
     // fast as a two-row register ring on every decode shape
     const int depth = o.depth == 2 ? 2 : 1;
-    const int cap = o.grid_cap > 0 ? o.grid_cap : (N > 32768 ? 1024 : 512);
+    // up to three workgroups per CU (two at four units per lane, where the register
+    // budget leaves three resident), looping when the rows need more; very tall
+    // matrices (lm_head) with eight per CU — measured on the decode shapes
+    const int cus = xs_cu_count();
+    const int cap = o.grid_cap > 0 ? o.grid_cap : (N > 32768 ? 8 * cus : upt >= 4 ? 2 * cus : 3 * cus);
     return y_f32 ? pick<float>(upt, depth, b, sb, x, M, lshift, cap, st)
                  : pick<f16>(upt, depth, b, sb, x, M, lshift, cap, st);
   }

@@ -226,8 +226,22 @@ struct FQ4K {
   // byte offset of unit u's super-block in the row (w) and in the scale row (s: none)
   __device__ static uint32_t woff(const QArgs&, int u) { return (uint32_t)(u >> 3) * BB; }
   __device__ static uint32_t soff(const QArgs&, int) { return 0; }
+  // Wave-row GEMV (raw buffer loads): the four lanes of a quad hold four units of the
+  // same super-block, so each loads one dword of the 16-byte header (d, dmin, scales)
+  // and share() broadcasts the four dwords across the quad — a quarter of the header
+  // bytes through the address unit instead of the whole header per lane.
   __device__ static Raw load_b(const Src& src, uint32_t wo, uint32_t, int u) {
-    return Raw{bld16(src.w, wo), bld16(src.w, wo + 16 + 16 * (u & 7))};
+    Raw r;
+    r.h = u32x4{bld4(src.w, wo + 4u * (uint32_t)(u & 3)), 0u, 0u, 0u};
+    r.q = bld16(src.w, wo + 16 + 16 * (u & 7));
+    return r;
+  }
+  __device__ static void share(Raw& r) {
+    const int v = (int)r.h.x;
+    r.h = u32x4{(uint32_t)__builtin_amdgcn_update_dpp(0, v, 0x00, 0xF, 0xF, false),    // quad_perm [0,0,0,0]
+                (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0x55, 0xF, 0xF, false),    // [1,1,1,1]
+                (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0xAA, 0xF, 0xF, false),    // [2,2,2,2]
+                (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0xFF, 0xF, 0xF, false)};   // [3,3,3,3]
   }
   // Quants enter v_dot2 as fp16 mantissa fields of 1.0: a low nibble (bits 0-3 of a
   // half) reads 1 + q/1024, a high nibble (bits 4-7) 1 + q/64, so one v_bfi_b32
