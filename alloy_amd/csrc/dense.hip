@@ -1153,6 +1153,15 @@ hipError_t launch_gemv_batched(int fmt, const WaveBatch& b, const void* x, bool 
 hipError_t launch_gemv_dot2(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
                             bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;
+  // GGUF blocks that are only 2-byte aligned (Q6_K always; Q5_0 / Q8_0 wire blocks
+  // once the matrix is large enough to amortise the staging) go through the
+  // LDS-staged kernel, which reads global memory with aligned 16-byte loads only
+  const bool unaligned_blocks = fmt == F_Q6_K || ((fmt == F_Q5_0 || fmt == F_Q8_0) && N * a.rb >= ((int64_t)16 << 20));
+  if (o.variant == 4 || (o.variant == 0 && unaligned_blocks)) {
+    const hipError_t e = launch_gemv_tile(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
+    if (e != hipErrorNotSupported) return e;
+    (void)hipGetLastError();
+  }
   if (o.variant == 0 || o.variant == 3) {
     // scale-row bytes (MLX scales/biases, split-layout scales) for the buffer views
     const uint32_t sb = scale_row_bytes(fmt, a);

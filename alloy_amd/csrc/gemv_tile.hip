@@ -1,0 +1,175 @@
+// M = 1 GEMV for GGUF formats with unaligned blocks (Q6_K 210 B, Q5_0 22 B, Q8_0 34 B
+// per block): the weight rows are copied through LDS so that global memory is read
+// with aligned 16-byte loads only, fp16 activations.
+//
+// A lane-per-unit GEMV that reads such blocks straight from global memory needs a
+// dozen 2- and 4-byte loads per unit (block starts are only 2-byte aligned), which
+// caps it far below HBM bandwidth.  Here a tile of R = 4 consecutive rows (one per
+// wave) is contiguous in memory and 16-byte aligned (checked on the host), so the
+// workgroup loads it with 16-byte loads into registers, one tile ahead of the one
+// being computed, and stores it to LDS; each wave then decodes its row from LDS
+// (2-byte-aligned LDS reads are cheap) with its 64 lanes splitting the row's units.
+// The activations are packed once per workgroup into per-unit records in LDS (the
+// format's v_dot2 pair order plus 16-element sums), read back per unit and row.
+// The grid is persistent (resident workgroups); workgroup bx walks tiles bx, bx +
+// grid, ...; rows past N read as zeros (buffer loads past the end) and are not stored.
+#include <atomic>
+
+#include "gemv.h"
+#include "launch.h"
+#include "xs.h"
+
+namespace alloy {
+
+namespace {
+
+constexpr int kTileRows = 4;    // one row per wave
+constexpr int kMaxCpl = 12;     // 16-byte chunks per lane per tile (48 KiB tiles)
+
+template <class F>
+constexpr int rec_words() {     // packed x record of one unit, in dwords (16-byte multiple)
+  return ((F::UE / 2 + F::UE / 16) + 3) / 4 * 4;
+}
+
+}  // namespace
+
+template <class F, typename YT>
+__global__ __launch_bounds__(256) void k_gemv_t(QArgs a, const f16* x, YT* y, int N, int cpl, int ntiles) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
+  constexpr int RW = rec_words<F>();
+  const int t = threadIdx.x, wv = t >> 6, lane = t & 63;
+  const int K = a.K, U = K / F::UE;
+  const uint32_t rb = (uint32_t)a.rb, tb = kTileRows * rb;
+  uint32_t* xrec = (uint32_t*)sm;                                   // U records of RW dwords
+  uint8_t* tile = sm + (uint32_t)U * RW * 4u;                       // cpl * 4 KiB
+  const __amdgpu_buffer_rsrc_t wr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, (int)((uint32_t)N * rb), ALLOY_RSRC_DW3);
+  const int grid = (int)gridDim.x;
+  int tl = (int)blockIdx.x;
+
+  // first tile's loads, then the activation records (their global reads overlap)
+  u32x4 v[kMaxCpl];
+  auto load_tile = [&](int tt) {
+    const uint32_t base = tt < ntiles ? (uint32_t)tt * tb : 0x80000000u;
+#pragma unroll
+    for (int c = 0; c < kMaxCpl; ++c)
+      if (c < cpl) {
+        const uint32_t o = (uint32_t)c * 4096u + (uint32_t)t * 16u;
+        v[c] = __builtin_amdgcn_raw_buffer_load_b128(wr, o < tb ? base + o : 0x80000000u, 0, 0);
+      }
+  };
+  load_tile(tl);
+  for (int u = t; u < U; u += 256) {
+    uint32_t xp[F::UE / 2];
+    float xg[F::UE / 16];
+    load_x_unit<F, f16>(x, u, xp, xg);
+    uint32_t* r = xrec + u * RW;
+#pragma unroll
+    for (int i = 0; i < F::UE / 2; i += 4) *(u32x4*)(r + i) = u32x4{xp[i], xp[i + 1], xp[i + 2], xp[i + 3]};
+    float g4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < F::UE / 16; ++i) g4[i & 3] = xg[i];
+    if constexpr (F::UE / 16 <= 4) {
+      *(u32x4*)(r + F::UE / 2) = u32x4{__builtin_bit_cast(uint32_t, g4[0]), __builtin_bit_cast(uint32_t, g4[1]),
+                                       __builtin_bit_cast(uint32_t, g4[2]), __builtin_bit_cast(uint32_t, g4[3])};
+    }
+  }
+
+  constexpr uint32_t esz = sizeof(YT);
+  const __amdgpu_buffer_rsrc_t yr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)y, (short)0, (int)((uint32_t)N * esz), ALLOY_RSRC_DW3);
+  for (; tl < ntiles; tl += grid) {
+#pragma unroll
+    for (int c = 0; c < kMaxCpl; ++c)
+      if (c < cpl) {
+        const uint32_t o = (uint32_t)c * 4096u + (uint32_t)t * 16u;
+        if (o < tb) *(u32x4*)(tile + o) = v[c];
+      }
+    load_tile(tl + grid);                 // next tile in flight during this one
+    lgkm_wait0();
+    wg_barrier();
+    const uint8_t* row = tile + (uint32_t)wv * rb;
+    float acc = 0.f;
+    for (int u = lane; u < U; u += 64) {
+      const uint32_t* r = xrec + u * RW;
+      uint32_t xp[F::UE / 2];
+      float xg[F::UE / 16];
+#pragma unroll
+      for (int i = 0; i < F::UE / 2; i += 4) {
+        const u32x4 q = *(const u32x4*)(r + i);
+        xp[i] = q.x; xp[i + 1] = q.y; xp[i + 2] = q.z; xp[i + 3] = q.w;
+      }
+      const u32x4 g = *(const u32x4*)(r + F::UE / 2);
+      // elements copied to scalars first: a bit_cast applied to a vector element
+      // directly picks element 0 in this compiler
+      const uint32_t g0 = g.x, g1 = g.y, g2 = g.z, g3 = g.w;
+      const float gg[4] = {__builtin_bit_cast(float, g0), __builtin_bit_cast(float, g1),
+                           __builtin_bit_cast(float, g2), __builtin_bit_cast(float, g3)};
+#pragma unroll
+      for (int i = 0; i < F::UE / 16; ++i) xg[i] = gg[i];
+      acc += F::dot(F::load_row(row, u), u, xp, xg);
+    }
+    acc = dpp_sum_rows(acc, 6);
+    const uint32_t n = (uint32_t)tl * kTileRows + (uint32_t)wv;
+    const uint32_t yo = lane == 63 && n < (uint32_t)N ? n * esz : 0x80000000u;
+    if constexpr (sizeof(YT) == 4) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc), yr, yo, 0, 0);
+    else __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (f16)acc), yr, yo, 0, 0);
+    wg_barrier();                         // every wave is done with the tile in LDS
+  }
+}
+
+namespace {
+
+template <class Kern>
+int tile_resident_per_cu(Kern kern, size_t lds) {
+  static std::atomic<int> cached[64];
+  const int key = (int)(lds >> 12) < 63 ? (int)(lds >> 12) : 63;
+  int v = cached[key].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, kern, 256, lds) != hipSuccess || v <= 0) v = 1;
+  cached[key].store(v, std::memory_order_relaxed);
+  return v;
+}
+
+template <class F>
+hipError_t run_tile(const QArgs& a, const void* x, void* y, bool y_f32, int64_t N64, const Opts& o,
+                    hipStream_t st) {
+  static_assert(F::UE / 16 <= 4, "packed x record holds at most four sums");
+  const int64_t tb = (int64_t)kTileRows * a.rb;
+  if (a.K % 256 || tb % 16 || ((uintptr_t)a.w & 15) || ((uintptr_t)x & 15)) return hipErrorNotSupported;
+  if ((uint64_t)N64 * (uint64_t)a.rb >= (1ull << 31) - (1u << 20)) return hipErrorNotSupported;
+  const int cpl = (int)((tb + 4095) / 4096);
+  const int U = a.K / F::UE;
+  const size_t lds = (size_t)U * rec_words<F>() * 4 + (size_t)cpl * 4096;
+  if (cpl > kMaxCpl || lds > 160 * 1024) return hipErrorNotSupported;
+  const int N = (int)N64;
+  const int ntiles = (N + kTileRows - 1) / kTileRows;
+  int grid = (y_f32 ? tile_resident_per_cu(k_gemv_t<F, float>, lds) : tile_resident_per_cu(k_gemv_t<F, f16>, lds)) *
+             xs_cu_count();
+  if (o.grid_cap > 0 && o.grid_cap < grid) grid = o.grid_cap;
+  if (grid > ntiles) grid = ntiles;
+  if (y_f32)
+    hipLaunchKernelGGL((k_gemv_t<F, float>), dim3((unsigned)grid), dim3(256), lds, st, a, (const f16*)x, (float*)y, N,
+                       cpl, ntiles);
+  else
+    hipLaunchKernelGGL((k_gemv_t<F, f16>), dim3((unsigned)grid), dim3(256), lds, st, a, (const f16*)x, (f16*)y, N,
+                       cpl, ntiles);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemv_tile(int fmt, const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32, int64_t M,
+                            int64_t N, const Opts& o, hipStream_t st) {
+  if (M != 1 || x_f32) return hipErrorNotSupported;
+  if (N == 0) return hipSuccess;
+  switch (fmt) {
+    case F_Q6_K: return run_tile<FQ6K>(a, x, y, y_f32, N, o, st);
+    case F_Q5_0: return run_tile<FQ50>(a, x, y, y_f32, N, o, st);
+    case F_Q8_0: return run_tile<FQ80>(a, x, y, y_f32, N, o, st);
+    case F_Q4_K: return run_tile<FQ4K>(a, x, y, y_f32, N, o, st);
+    default: return hipErrorNotSupported;
+  }
+}
+
+}  // namespace alloy

@@ -21,7 +21,7 @@ struct Opts {
   int grid_cap = 0;        // dot2 GEMV: max workgroups (grid-stride beyond)
   int row_groups = 0;      // MFMA GEMV: 16-row groups per workgroup (1, 2)
   int depth = 0;           // dot2 GEMV: rows of weights in flight per thread (2, 3, 4)
-  int variant = 0;         // dot2 GEMV: 0 automatic, 1 register ring, 2 LDS-staged tiles
+  int variant = 0;         // dot2 GEMV: 0 automatic, 1 register ring, 2 LDS-staged tiles, 4 aligned-load LDS tiles
 };
 
 // Several weight matrices (same format and K) against one x in a single launch:
@@ -49,6 +49,10 @@ hipError_t launch_embedding(int fmt, const QArgs& a, const void* ids, bool ids64
 
 hipError_t launch_dequant(int fmt, const QArgs& a, void* out, bool out_f16, int64_t row0,
                           int64_t nrows, hipStream_t st);
+// M = 1 GEMV with the rows copied through LDS by aligned 16-byte loads (GGUF wire
+// formats; fp16 activations).  hipErrorNotSupported when the shape does not fit.
+hipError_t launch_gemv_tile(int fmt, const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32, int64_t M,
+                            int64_t N, const Opts& o, hipStream_t st);
 hipError_t launch_gemv_dot2(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
                             bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st);
 hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
