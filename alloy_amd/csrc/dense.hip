@@ -540,26 +540,6 @@ __global__ __launch_bounds__(256) void k_gemm(QArgs a, const XT* x, int M, void*
 // rounded once to fp16.
 constexpr int QBK = 64, QLD = 72;
 
-// mix_lo* start a dword (the high half is left undefined for a following mix_hi*)
-__device__ __forceinline__ uint32_t mix_lo(uint32_t q, float s, float c) {               // q.lo
-  uint32_t d;
-  asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(q), "v"(s), "v"(c));
-  return d;
-}
-__device__ __forceinline__ uint32_t mix_hi(uint32_t d, uint32_t q, float s, float c) {   // q.lo
-  asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "+v"(d) : "v"(q), "v"(s), "v"(c));
-  return d;
-}
-__device__ __forceinline__ uint32_t mix_lo_h(uint32_t q, float s, float c) {             // q.hi
-  uint32_t d;
-  asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(q), "v"(s), "v"(c));
-  return d;
-}
-__device__ __forceinline__ uint32_t mix_hi_h(uint32_t d, uint32_t q, float s, float c) { // q.hi
-  asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(d) : "v"(q), "v"(s), "v"(c));
-  return d;
-}
-
 // MI x NI: 32x32 MFMA tiles per wave; the 8 waves sit as 2 (x rows) x 4 (weight rows),
 // so a workgroup tile is QBM = 64*MI x QBN = 128*NI.
 template <int MI, int NI, typename YT>
