@@ -15,7 +15,9 @@ graph replays (HIP events on the replay stream, synchronized on both sides).
 launch duration per weight shape comes from a graph of all 28 launches of that
 shape (each layer's own weights, so HBM-cold), timed the same way.  ``cpu_baseline``
 times the CPU oracle (NumPy dequant + PyTorch-CPU fp32 matmul) on one layer.
-``prefill_gemm`` reports the Q4_K MFMA GEMM at M=2048 on the three config-4 shapes.
+``prefill_gemm`` reports the Q4_K MFMA GEMM at M=2048 on the three config-4 shapes;
+``other_configs`` the remaining BASELINE configurations (1, 3 and 5) with their weight
+GB/s, each timed over rotating weight copies larger than the Infinity Cache.
 """
 
 from __future__ import annotations
@@ -212,6 +214,72 @@ def prefill_gemm(dev, qmm, M=2048, reps=10):
     return out
 
 
+def _rotating_time(dev, fn_for, copies, reps=5):
+    """Average seconds per call of fn_for(copy) over a graph that cycles through
+    `copies` (together larger than the 256 MB Infinity Cache, so weights come from HBM)."""
+    import torch
+
+    seq = copies * max(1, 24 // len(copies))
+    stream = torch.cuda.current_stream(dev)
+    g = capture(lambda: [fn_for(c) for c in seq], dev)
+    t = time_replays(g, reps, 2, stream) / (reps * len(seq))
+    del g
+    return t
+
+
+def other_configs(dev, qmm):
+    """The other BASELINE configurations, on the GPU: config 1 (Q8_0 4096x4096, M=1,
+    fp32 out), config 3 (Q6_K and Q5_0 at Llama-3-8B shapes, M=1 and M=8) and config 5
+    (MLX 4-bit MoE, 128 experts, top-8, H=2048, I=768, T in {1, 16, 256})."""
+    import torch
+
+    from alloy_amd import formats, synth
+
+    out = {}
+
+    def gemv_case(fmt, K, N, M, seed):
+        nbytes = formats.row_bytes(fmt, K) * N
+        ncopy = max(2, -(-320_000_000 // nbytes))
+        ws = [synth.torch_blocks(fmt, N, K, seed + i, dev) for i in range(ncopy)]
+        x = synth.torch_x(M, K, seed, dev)
+        y = torch.empty((M, N), dtype=torch.float32, device=dev)
+        t = _rotating_time(dev, lambda w: qmm(fmt, x, w, out=y), ws)
+        del ws
+        return {"us": round(t * 1e6, 2), "GBps": round(nbytes / t / 1e9, 1),
+                "frac_hbm_peak": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+
+    out["config1_q8_0_4096x4096_M1"] = gemv_case("q8_0", 4096, 4096, 1, 300)
+    for fmt in ("q6_k", "q5_0"):
+        for M in (1, 8):
+            out[f"config3_{fmt}_M{M}"] = {f"{K}x{N}": gemv_case(fmt, K, N, M, 400 + K + N)
+                                           for K, N in [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)]}
+    # config 5: MLX MoE
+    E, k, H, I, gs = 128, 8, 2048, 768, 64
+    experts = []
+    for c in range(3):
+        g = torch.Generator(device=dev)
+        g.manual_seed(500 + c)
+        experts.append((
+            torch.randint(0, 256, (E, 2 * I, H // 2), dtype=torch.uint8, device=dev, generator=g),
+            (torch.rand((E, 2 * I, H // gs), device=dev, generator=g) * 0.01).half(),
+            ((torch.rand((E, 2 * I, H // gs), device=dev, generator=g) - 0.5) * 0.02).half(),
+            torch.randint(0, 256, (E, H, I // 2), dtype=torch.uint8, device=dev, generator=g),
+            (torch.rand((E, H, I // gs), device=dev, generator=g) * 0.01).half(),
+            ((torch.rand((E, H, I // gs), device=dev, generator=g) - 0.5) * 0.02).half()))
+    per_expert = sum(t.numel() * t.element_size() for t in experts[0]) // E
+    moe = {}
+    for T in (1, 16, 256):
+        x = synth.torch_x(T, H, 600 + T, dev)
+        lg = torch.randn((T, E), device=dev, generator=torch.Generator(device=dev).manual_seed(T))
+        t = _rotating_time(dev, lambda c: torch.ops.alloy.mlx_moe_routed(x, lg, *c, E, k, I), experts)
+        touched = int(torch.unique(torch.topk(lg, k, dim=1).indices).numel())
+        moe[f"T{T}"] = {"us": round(t * 1e6, 1), "experts_touched": touched,
+                        "GBps_touched_weights": round(touched * per_expert / t / 1e9, 1)}
+    out["config5_mlx_moe"] = moe
+    del experts
+    return out
+
+
 def traffic_from_profiles():
     """HBM bytes per launch of the dominant kernel, from the committed PMC summary
     (a line ``traffic_bytes_per_launch = N`` in profiles/q4k_gemv_decode_pmc.md)."""
@@ -247,6 +315,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the other BASELINE configurations")
     ap.add_argument("--decode-only", action="store_true",
                     help="time the decode step only (no per-shape, prefill or CPU legs)")
     ap.add_argument("--eager", action="store_true",
@@ -320,6 +389,9 @@ def main():
     if prefill:
         log(json.dumps(prefill))
     cpu = None if args.no_cpu else cpu_baseline()
+    configs = None if args.no_configs else other_configs(dev, qmm)
+    if configs:
+        log(json.dumps(configs))
 
     rec = {
         "metric": "Q4_K decode GEMV weight GB/s (% HBM peak); Q4_K prefill GEMM TFLOP/s",
@@ -345,6 +417,7 @@ def main():
         "cpu_baseline": cpu,
         "prefill_gemm": prefill,
         "batched_step": batched,
+        "other_configs": configs,
     }
     print(json.dumps(rec))
 
