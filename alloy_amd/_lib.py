@@ -42,6 +42,9 @@ _vp, _i32, _i64, _sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c
 # name -> (restype, argtypes); mirrors include/alloy_amd.h
 SIGNATURES = {
     "alloy_qmm": (_i32, [_i32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _i32, _i64, _vp]),
+    "alloy_qmm_ws": (_i32, [_i32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _i32, _i64, _vp,
+                            _i64, _vp]),
+    "alloy_gemm_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64]),
     "alloy_gguf_q4_k_mm": (_i32, [_vp, _i32, _vp, _vp, _i32, _i64, _i64, _i64, _vp]),
     "alloy_gguf_q6_k_mm": (_i32, [_vp, _i32, _vp, _vp, _i32, _i64, _i64, _i64, _vp]),
     "alloy_gguf_q8_0_mm": (_i32, [_vp, _i32, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp]),

@@ -98,10 +98,23 @@ extern "C" {
 const char* alloy_last_error(void) { return g_err.c_str(); }
 const char* alloy_version(void) { return "alloy_amd 0.1.0 (gfx950)"; }
 
+int64_t alloy_gemm_workspace_bytes(alloy_format fmt, int64_t M, int64_t N, int64_t K) {
+  if (M <= 16 || M > 65535LL * 128 || N <= 0 || K <= 0) return 0;
+  return alloy::gemm_workspace_bytes((int)fmt, M, N, K);
+}
+
 alloy_status alloy_qmm(alloy_format fmt, const void* w, const void* aux, const void* scales,
                        const void* biases, int32_t group_size, const void* x, alloy_dtype x_dtype,
                        void* y, alloy_dtype y_dtype, int64_t M, int64_t N, int64_t K,
                        alloy_path path, int64_t opts, void* stream) {
+  return alloy_qmm_ws(fmt, w, aux, scales, biases, group_size, x, x_dtype, y, y_dtype, M, N, K, path, opts, nullptr,
+                      0, stream);
+}
+
+alloy_status alloy_qmm_ws(alloy_format fmt, const void* w, const void* aux, const void* scales,
+                          const void* biases, int32_t group_size, const void* x, alloy_dtype x_dtype,
+                          void* y, alloy_dtype y_dtype, int64_t M, int64_t N, int64_t K,
+                          alloy_path path, int64_t opts, void* ws, int64_t ws_bytes, void* stream) {
   QArgs a;
   alloy_status s = make_args((int)fmt, w, aux, scales, biases, group_size, K, a);
   if (s != ALLOY_OK) return s;
@@ -135,7 +148,8 @@ alloy_status alloy_qmm(alloy_format fmt, const void* w, const void* aux, const v
       return hip_status(alloy::launch_gemv_mfma((int)fmt, a, x, xf, y, yf, M, N, o, st), "gemv_mfma launch");
     case alloy::P_GEMM:
       if (M > 65535LL * 128) return fail(ALLOY_E_SHAPE, "GEMM: M=%lld too large", (long long)M);
-      return hip_status(alloy::launch_gemm((int)fmt, a, x, xf, y, yf, M, N, o, st), "gemm launch");
+      if (ws_bytes < 0 || (ws_bytes > 0 && !ws)) return fail(ALLOY_E_ARG, "bad workspace (%lld bytes)", (long long)ws_bytes);
+      return hip_status(alloy::launch_gemm((int)fmt, a, x, xf, y, yf, M, N, o, ws, ws_bytes, st), "gemm launch");
     default:
       return fail(ALLOY_E_ARG, "unknown path code %d", (int)path);
   }

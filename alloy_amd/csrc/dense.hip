@@ -543,11 +543,15 @@ constexpr int QBK = 64, QLD = 72;
 // MI x NI: 32x32 MFMA tiles per wave; the 8 waves sit as 2 (x rows) x 4 (weight rows),
 // so a workgroup tile is QBM = 64*MI x QBN = 128*NI.
 template <int MI, int NI, typename YT>
-__global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, YT* y, int N) {
+__global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, YT* y, int N, int nsb) {
   constexpr int QBM = 64 * MI, QBN = 128 * NI, AC = QBM / 64;   // AC: x chunks per thread
   __shared__ __attribute__((aligned(16))) f16 As[2][QBM][QLD];
   __shared__ __attribute__((aligned(16))) f16 Bs[2][QBN][QLD];
-  const int K = a.K, KT = K / QBK;
+  // nsb > 0: split K — this workgroup (blockIdx.z) covers super-blocks
+  // [z*nsb, (z+1)*nsb) and writes its fp32 partial tile to slice z of y
+  const int K = a.K, KT = nsb > 0 ? 4 * nsb : K / QBK;
+  const uint32_t kb = nsb > 0 ? (uint32_t)blockIdx.z * (uint32_t)nsb : 0u;
+  if (nsb > 0) y += (size_t)blockIdx.z * (size_t)M * (size_t)N;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int wm = wave >> 2, wn = wave & 3;
   const int m0 = (int)blockIdx.y * QBM, n0 = (int)blockIdx.x * QBN;
@@ -564,7 +568,7 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, 
     const int c = tid + 512 * i;
     arow[i] = c >> 3;
     acol[i] = (c & 7) * 8;
-    xoff[i] = ((uint32_t)(m0 + arow[i]) * (uint32_t)K + (uint32_t)acol[i]) * 2u;
+    xoff[i] = ((uint32_t)(m0 + arow[i]) * (uint32_t)K + 256u * kb + (uint32_t)acol[i]) * 2u;
   }
   // weight tile: row br; thread half bh owns quant bytes 32p + 16bh .. +15 of every
   // pair p, i.e. elements 16bh + [0,16) (low nibbles, sub-block 2p) and
@@ -573,7 +577,7 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, 
   // burst every four steps, so each weight line is fetched into L1 once.  With
   // QBN = 128 the upper half of the threads mirror the lower half's rows.
   const int br = (tid >> 1) & (QBN - 1), bh = tid & 1;
-  const uint32_t wrow = (uint32_t)(n0 + br) * rb;
+  const uint32_t wrow = (uint32_t)(n0 + br) * rb + 144u * kb;
 
   struct Blk { u32x4 hd, q[4]; };          // this thread's bytes of one super-block
   auto bload = [&](int sb, Blk& r) {       // past the end: in-bounds garbage or zeros
@@ -1495,32 +1499,105 @@ hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, 
   return by_fmt<GemvMfmaRun>(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
 }
 
+// Sum of the S fp32 split-K partial slices, in slice order (deterministic).
+template <typename YT>
+__global__ __launch_bounds__(256) void k_splitk_sum(const float* ws, int S, int64_t mn, YT* y) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= mn) return;
+  f32x4 acc = *(const f32x4*)(ws + i);
+  for (int z = 1; z < S; ++z) acc += *(const f32x4*)(ws + (int64_t)z * mn + i);
+  if constexpr (sizeof(YT) == 4) {
+    *(f32x4*)((float*)y + i) = acc;
+  } else {
+    const float a0 = acc[0], a1 = acc[1], a2 = acc[2], a3 = acc[3];   // elements copied out first
+    *(f16x4*)((f16*)y + i) = f16x4{(f16)a0, (f16)a1, (f16)a2, (f16)a3};
+  }
+}
+
+// Q4_K GEMM plan: tile kind (0 = 256x256, 1 = 128x256, 2 = 128x128, 3 = 64x256,
+// 4 = 64x128) and K splits S.  Each kind's measured full-chip rate (TFLOP/s on
+// MI355X) is scaled by the fraction of CU slots its tile count x S fills in the last
+// round of workgroups; a split adds the partial-sum pass ((S+1) fp32 M x N tiles of
+// HBM traffic) and one launch.  S divides the super-blocks, at least two per split.
+struct GemmPlan { int kind, splits; };
+static GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K, bool allow_split) {
+  const int cus = xs_cu_count();
+  const int bm[5] = {256, 128, 128, 64, 64}, bn[5] = {256, 256, 128, 256, 128};
+  const double rate[5] = {1000e12, 790e12, 600e12, 590e12, 420e12};
+  const double flops = 2.0 * (double)M * (double)N * (double)K;
+  const int64_t sb = K / 256;
+  GemmPlan best{0, 1};
+  double best_t = 1e30;
+  for (int k = 0; k < 5; ++k) {
+    const int64_t tl = ((M + bm[k] - 1) / bm[k]) * ((N + bn[k] - 1) / bn[k]);
+    for (int S = 1; S <= (allow_split ? 4 : 1); ++S) {
+      if (S > 1 && (sb % S || sb / S < 2)) continue;
+      const int64_t wg = tl * S, rounds = (wg + cus - 1) / cus;
+      double t = flops / (rate[k] * (double)wg / (double)(rounds * cus));
+      if (S > 1) t += (double)(S + 1) * (double)M * (double)N * 4.0 / 5e12 + 2e-6;
+      if (t < best_t) { best_t = t; best = GemmPlan{k, S}; }
+    }
+  }
+  return best;
+}
+
+static bool gemm_q4k_fits(int64_t M, int64_t N, const QArgs& a) {   // 32-bit buffer offsets
+  return (uint64_t)M * (uint64_t)a.K * 2u < (1ull << 31) && (uint64_t)N * (uint64_t)a.rb < (1ull << 31) &&
+         (uint64_t)M * (uint64_t)N * 4u < (1ull << 31);
+}
+
+int64_t gemm_workspace_bytes(int fmt, int64_t M, int64_t N, int64_t K) {
+  if (fmt != F_Q4_K || M <= 64 || K % 256) return 0;
+  const GemmPlan p = gemm_plan(M, N, K, true);
+  return p.splits > 1 ? (int64_t)p.splits * M * N * 4 : 0;
+}
+
 template <class F>
 struct GemmRun {
   static hipError_t run(const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32, int64_t M,
-                        int64_t N, const Opts& o, hipStream_t st) {
+                        int64_t N, const Opts& o, void* ws, int64_t ws_bytes, hipStream_t st) {
     if constexpr (std::is_same<F, FQ4K>::value) {
-      // 256x256 tiles once there are x rows enough to fill them; 32-bit buffer offsets
-      const bool fits = (uint64_t)M * (uint64_t)a.K * 2u < (1ull << 31) && (uint64_t)N * (uint64_t)a.rb < (1ull << 31) &&
-                        (uint64_t)M * (uint64_t)N * 4u < (1ull << 31);
-      if (!x_f32 && fits && (M > 64 || o.variant >= 4) && o.variant != 1) {
-        // largest tile that still gives every CU a workgroup (256 CUs), else the smallest
-        auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-        int kind = o.variant >= 4 ? o.variant - 4 : (tiles(256, 256) >= 256 ? 0 : tiles(128, 256) >= 256 ? 1 : 2);
+      if (!x_f32 && gemm_q4k_fits(M, N, a) && (M > 64 || o.variant >= 4) && o.variant != 1) {
+        GemmPlan p = o.variant >= 4 ? GemmPlan{o.variant - 4, 1} : gemm_plan(M, N, a.K, ws != nullptr);
+        if (p.splits > 1 &&
+            (ws_bytes < (int64_t)p.splits * M * N * 4 || ((uintptr_t)ws & 15) || ((uintptr_t)y & 15) || (M * N) % 4))
+          p = gemm_plan(M, N, a.K, false);
+        const int nsb = p.splits > 1 ? (int)(a.K / 256 / p.splits) : 0;
         auto go = [&](auto mi, auto ni) {
           constexpr int MI = decltype(mi)::value, NI = decltype(ni)::value;
-          const dim3 grid((unsigned)((N + 128 * NI - 1) / (128 * NI)), (unsigned)((M + 64 * MI - 1) / (64 * MI)));
-          if (y_f32)
-            hipLaunchKernelGGL((k_gemm_q4k<MI, NI, float>), grid, dim3(512), 0, st, a, (const f16*)x, (int)M, (float*)y, (int)N);
+          const dim3 grid((unsigned)((N + 128 * NI - 1) / (128 * NI)), (unsigned)((M + 64 * MI - 1) / (64 * MI)),
+                          (unsigned)p.splits);
+          if (p.splits > 1)
+            hipLaunchKernelGGL((k_gemm_q4k<MI, NI, float>), grid, dim3(512), 0, st, a, (const f16*)x, (int)M,
+                               (float*)ws, (int)N, nsb);
+          else if (y_f32)
+            hipLaunchKernelGGL((k_gemm_q4k<MI, NI, float>), grid, dim3(512), 0, st, a, (const f16*)x, (int)M,
+                               (float*)y, (int)N, 0);
           else
-            hipLaunchKernelGGL((k_gemm_q4k<MI, NI, f16>), grid, dim3(512), 0, st, a, (const f16*)x, (int)M, (f16*)y, (int)N);
+            hipLaunchKernelGGL((k_gemm_q4k<MI, NI, f16>), grid, dim3(512), 0, st, a, (const f16*)x, (int)M,
+                               (f16*)y, (int)N, 0);
+          hipError_t e = hipGetLastError();
+          if (e != hipSuccess || p.splits == 1) return e;
+          const int64_t mn = M * N, blocks = (mn / 4 + 255) / 256;
+          if (y_f32)
+            hipLaunchKernelGGL(k_splitk_sum<float>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)ws,
+                               p.splits, mn, (float*)y);
+          else
+            hipLaunchKernelGGL(k_splitk_sum<f16>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)ws,
+                               p.splits, mn, (f16*)y);
           return hipGetLastError();
         };
-        if (kind == 0) return go(std::integral_constant<int, 4>(), std::integral_constant<int, 2>());
-        if (kind == 1) return go(std::integral_constant<int, 2>(), std::integral_constant<int, 2>());
-        return go(std::integral_constant<int, 2>(), std::integral_constant<int, 1>());
+        switch (p.kind) {
+          case 0: return go(std::integral_constant<int, 4>(), std::integral_constant<int, 2>());
+          case 1: return go(std::integral_constant<int, 2>(), std::integral_constant<int, 2>());
+          case 3: return go(std::integral_constant<int, 1>(), std::integral_constant<int, 2>());
+          case 4: return go(std::integral_constant<int, 1>(), std::integral_constant<int, 1>());
+          default: return go(std::integral_constant<int, 2>(), std::integral_constant<int, 1>());
+        }
       }
     }
+    (void)ws;
+    (void)ws_bytes;
     dim3 grid((unsigned)((N + GBN - 1) / GBN), (unsigned)((M + GBM - 1) / GBM));
     if (x_f32)
       hipLaunchKernelGGL((k_gemm<F, float>), grid, dim3(256), 0, st, a, (const float*)x, (int)M, y, (int)y_f32, N);
@@ -1531,9 +1608,9 @@ struct GemmRun {
 };
 
 hipError_t launch_gemm(int fmt, const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32,
-                       int64_t M, int64_t N, const Opts& o, hipStream_t st) {
+                       int64_t M, int64_t N, const Opts& o, void* ws, int64_t ws_bytes, hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;
-  return by_fmt<GemmRun>(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
+  return by_fmt<GemmRun>(fmt, a, x, x_f32, y, y_f32, M, N, o, ws, ws_bytes, st);
 }
 
 }  // namespace alloy

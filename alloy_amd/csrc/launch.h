@@ -57,8 +57,11 @@ hipError_t launch_gemv_dot2(int fmt, const QArgs& a, const void* x, bool x_f32, 
                             bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st);
 hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
                             bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st);
+// Prefill GEMM.  ws (ws_bytes): optional fp32 workspace for the Q4_K split-K plan,
+// gemm_workspace_bytes() of it (0: no split); without it the plan has no split.
 hipError_t launch_gemm(int fmt, const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32,
-                       int64_t M, int64_t N, const Opts& o, hipStream_t st);
+                       int64_t M, int64_t N, const Opts& o, void* ws, int64_t ws_bytes, hipStream_t st);
+int64_t gemm_workspace_bytes(int fmt, int64_t M, int64_t N, int64_t K);
 
 // Gated pair y = act(x G^T) * (x U^T) (act 0 silu, 1 gelu in tanh form): one fused
 // launch for M <= 16 when glu_fused_supported(), else two products into fp32

@@ -131,10 +131,17 @@ def qmm(fmt: str, x: torch.Tensor, w: torch.Tensor, *, scales=None, biases=None,
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=dev)
     with torch.cuda.device(dev):
-        _lib.call("alloy_qmm", _lib.FMT[fmt], _p(w), _p(aux), _p(scales), _p(biases), group_size,
+        ws = gemm_workspace(fmt, M, N, K, dev) if path in ("auto", "gemm") else None
+        _lib.call("alloy_qmm_ws", _lib.FMT[fmt], _p(w), _p(aux), _p(scales), _p(biases), group_size,
                   _p(x), _dt(x.dtype, "activations"), _p(out), _dt(out.dtype, "output"), M, N, K,
-                  _lib.PATH[path], opts, _stream(dev))
+                  _lib.PATH[path], opts, _p(ws), 0 if ws is None else ws.numel(), _stream(dev))
     return out
+
+
+def gemm_workspace(fmt: str, M: int, N: int, K: int, dev) -> torch.Tensor | None:
+    """The split-K workspace the prefill GEMM plan wants for this shape (None: no split)."""
+    need = int(_lib.lib().alloy_gemm_workspace_bytes(_lib.FMT[fmt], M, N, K)) if M > 16 else 0
+    return torch.empty(need, dtype=torch.uint8, device=dev) if need > 0 else None
 
 
 def dequant(fmt: str, w: torch.Tensor, K: int, *, scales=None, biases=None, aux=None, group_size: int = 0,
@@ -457,6 +464,9 @@ def _run_named(name: str, activations: torch.Tensor, bufs: list[torch.Tensor], M
 
 def _q4_k(activations, blocks):
     M, N, K = shape_gguf_blocks("q4_k", activations, blocks)
+    if M > 16:            # prefill: the GEMM may split K into a workspace
+        _same_device(activations, blocks)
+        return qmm("q4_k", activations, blocks.contiguous(), N=N)
     return _run_named("alloy_gguf_q4_k_mm", activations, [blocks], M, N, K)
 
 

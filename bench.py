@@ -15,7 +15,7 @@ graph replays (HIP events on the replay stream, synchronized on both sides).
 launch duration per weight shape comes from a graph of all 28 launches of that
 shape (each layer's own weights, so HBM-cold), timed the same way.  ``cpu_baseline``
 times the CPU oracle (NumPy dequant + PyTorch-CPU fp32 matmul) on one layer.
-``prefill_gemm`` reports the Q4_K MFMA GEMM at M=2048 on the three config-4 shapes;
+``prefill_gemm`` reports the Q4_K MFMA GEMM at M = 512, 2048, 4096 on the three config-4 shapes;
 ``other_configs`` the remaining BASELINE configurations (1, 3 and 5) with their weight
 GB/s, each timed over rotating weight copies larger than the Infinity Cache.
 """
@@ -194,13 +194,13 @@ def cpu_baseline(seconds_target=15.0):
     }
 
 
-def prefill_gemm(dev, qmm, M=2048, reps=10):
+def prefill_gemm(dev, qmm, Ms=(512, 2048, 4096), reps=10):
     import torch
 
     from alloy_amd import synth
 
     out = []
-    for K, N in PREFILL:
+    for M, (K, N) in [(M, kn) for M in Ms for kn in PREFILL]:
         w = synth.torch_blocks("q4_k", N, K, 77 + N, dev)
         x = synth.torch_x(M, K, 78 + K, dev)
         y = torch.empty((M, N), dtype=torch.float32, device=dev)
@@ -230,7 +230,8 @@ def _rotating_time(dev, fn_for, copies, reps=5):
 def other_configs(dev, qmm):
     """The other BASELINE configurations, on the GPU: config 1 (Q8_0 4096x4096, M=1,
     fp32 out), config 3 (Q6_K and Q5_0 at Llama-3-8B shapes, M=1 and M=8) and config 5
-    (MLX 4-bit MoE, 128 experts, top-8, H=2048, I=768, T in {1, 16, 256})."""
+    (MLX 4-bit MoE, 128 experts, top-8, H=2048, I=768, T in {1, 16, 256}); config 2 is
+    repeated at M=4 and M=16 (its distinct shapes)."""
     import torch
 
     from alloy_amd import formats, synth
@@ -249,6 +250,9 @@ def other_configs(dev, qmm):
                 "frac_hbm_peak": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
 
     out["config1_q8_0_4096x4096_M1"] = gemv_case("q8_0", 4096, 4096, 1, 300)
+    for M in (4, 16):
+        out[f"config2_q4_k_M{M}"] = {f"{K}x{N}": gemv_case("q4_k", K, N, M, 350 + K + N)
+                                     for _, K, N in LLAMA32_3B[:2] + LLAMA32_3B[4:5] + LLAMA32_3B[6:] + [LM_HEAD]}
     for fmt in ("q6_k", "q5_0"):
         for M in (1, 8):
             out[f"config3_{fmt}_M{M}"] = {f"{K}x{N}": gemv_case(fmt, K, N, M, 400 + K + N)

@@ -78,10 +78,12 @@ typedef enum {
  *   bits 28-31 MFMA GEMV row groups, bits 32-35 rows of weights in flight per
  *   thread of the v_dot2 GEMV (2, 3 or 4), bits 36-39 the kernel variant (0
  *   automatic).  GEMV: 1 register ring with an LDS row combine, 2 LDS-staged row
- *   tiles, 3 wave rows with buffer loads and DPP reductions.  MFMA GEMV (M <= 16):
- *   1 16x16x32 tiles, 5 Q4_K 4x4x4 broadcast tiles, 6 Q4_K x-stationary tiles,
- *   7 x-stationary tiles of any format that has them.  GEMM: 1 generic 128x128
- *   tiles, 4 / 5 / 6 Q4_K tiles of 256x256 / 128x256 / 128x128.
+ *   tiles, 3 wave rows with buffer loads and DPP reductions, 4 rows staged through
+ *   LDS by aligned 16-byte loads (Q6_K, Q5_0, Q8_0, Q4_K wire blocks).  MFMA GEMV
+ *   (M <= 16): 1 16x16x32 tiles, 5 Q4_K 4x4x4 broadcast tiles, 6 Q4_K x-stationary
+ *   tiles, 7 x-stationary tiles of any format that has them.  GEMM: 1 generic
+ *   128x128 tiles, 4 / 5 / 6 / 7 / 8 Q4_K tiles of 256x256 / 128x256 / 128x128 /
+ *   64x256 / 64x128 (no K split).
  * No reference counterpart as a single op: the reference dispatches per format
  * (packages/alloy-torch/src/alloy_torch/ops/linalg.py:346-739); the named entry
  * points below are the per-op replacements and all route here.
@@ -90,6 +92,21 @@ alloy_status alloy_qmm(alloy_format fmt, const void* w, const void* aux, const v
                        const void* biases, int32_t group_size, const void* x, alloy_dtype x_dtype,
                        void* y, alloy_dtype y_dtype, int64_t M, int64_t N, int64_t K,
                        alloy_path path, int64_t opts, void* stream);
+
+/*
+ * alloy_qmm with a caller workspace for the prefill GEMM: when the Q4_K GEMM would
+ * leave CUs idle (few output tiles, e.g. M = 512), it splits K into S slices whose
+ * fp32 partial products go to ws (S*M*N*4 bytes, 16-byte aligned, y 16-byte
+ * aligned) and are summed in slice order (deterministic).  ws = NULL or too small:
+ * no split.  alloy_gemm_workspace_bytes() returns the bytes the plan wants for this
+ * shape (0 when it does not split).  No reference counterpart (the reference has no
+ * K split); for callers of the GEMM path that can provide scratch memory.
+ */
+int64_t alloy_gemm_workspace_bytes(alloy_format fmt, int64_t M, int64_t N, int64_t K);
+alloy_status alloy_qmm_ws(alloy_format fmt, const void* w, const void* aux, const void* scales,
+                          const void* biases, int32_t group_size, const void* x, alloy_dtype x_dtype,
+                          void* y, alloy_dtype y_dtype, int64_t M, int64_t N, int64_t K,
+                          alloy_path path, int64_t opts, void* ws, int64_t ws_bytes, void* stream);
 
 /* torch.ops.alloy.gguf_q4_k_mm(activations, blocks) — custom_ops.py:47-49 */
 alloy_status alloy_gguf_q4_k_mm(const void* x, alloy_dtype x_dtype, const void* blocks, void* y,
