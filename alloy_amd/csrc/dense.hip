@@ -1484,9 +1484,16 @@ static int mfma_variant(int fmt, int64_t M, int64_t N, int64_t K) {
 hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
                             bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;
-  const int v = o.variant ? o.variant : mfma_variant(fmt, M, N, a.K);
+  // few activation rows on few or unaligned rows: the LDS-staged v_dot2 kernel (weights
+  // read once, decoded once per row and token) beats the MFMA kernels' fixed cost —
+  // measured on the BASELINE decode shapes at M = 2, 4, 8
+  const bool unaligned = fmt == F_Q6_K || fmt == F_Q5_0 || fmt == F_Q8_0;
+  const bool tile_small_m = unaligned ? (M == 2 || M * N <= 8192)
+                                      : fmt == F_Q4_K && ((M == 2 && (N <= 1024 || a.K >= 8192)) || (M <= 4 && N <= 1024));
+  const int v = o.variant ? o.variant : tile_small_m ? 9 : mfma_variant(fmt, M, N, a.K);
   hipError_t e = hipErrorNotSupported;
-  if (v == 7) e = launch_gemv_xs(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
+  if (v == 9) e = launch_gemv_tile(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
+  else if (v == 7) e = launch_gemv_xs(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
   else if (v == 6 && fmt == F_Q4_K) e = launch_gemv_xs_q4k(a, x, x_f32, y, y_f32, M, N, o, st);
   else if (v == 5 && fmt == F_Q4_K) e = launch_gemv_q4k_m4(a, x, x_f32, y, y_f32, M, N, o, st);
   if (e != hipErrorNotSupported) return e;

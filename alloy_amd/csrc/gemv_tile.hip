@@ -1,6 +1,7 @@
-// M = 1 GEMV for GGUF formats with unaligned blocks (Q6_K 210 B, Q5_0 22 B, Q8_0 34 B
-// per block): the weight rows are copied through LDS so that global memory is read
-// with aligned 16-byte loads only, fp16 activations.
+// GEMV for M <= 8 activation rows over GGUF formats with unaligned blocks (Q6_K 210 B,
+// Q5_0 22 B, Q8_0 34 B per block): the weight rows are copied through LDS so that
+// global memory is read with aligned 16-byte loads only (once, whatever M), fp16
+// activations.
 //
 // A lane-per-unit GEMV that reads such blocks straight from global memory needs a
 // dozen 2- and 4-byte loads per unit (block starts are only 2-byte aligned), which
@@ -9,8 +10,9 @@
 // workgroup loads it with 16-byte loads into registers, one tile ahead of the one
 // being computed, and stores it to LDS; each wave then decodes its row from LDS
 // (2-byte-aligned LDS reads are cheap) with its 64 lanes splitting the row's units.
-// The activations are packed once per workgroup into per-unit records in LDS (the
-// format's v_dot2 pair order plus 16-element sums), read back per unit and row.
+// The activations are packed once per workgroup into per-(token, unit) records in
+// LDS (the format's v_dot2 pair order plus 16-element sums), read back per unit, row
+// and token.
 // The grid is persistent (resident workgroups); workgroup bx walks tiles bx, bx +
 // grid, ...; rows past N read as zeros (buffer loads past the end) and are not stored.
 #include <atomic>
@@ -25,6 +27,7 @@ namespace {
 
 constexpr int kTileRows = 4;    // one row per wave
 constexpr int kMaxCpl = 12;     // 16-byte chunks per lane per tile (48 KiB tiles)
+constexpr int kMaxTokens = 8;   // activation rows (records of each live in LDS)
 
 template <class F>
 constexpr int rec_words() {     // packed x record of one unit, in dwords (16-byte multiple)
@@ -34,14 +37,14 @@ constexpr int rec_words() {     // packed x record of one unit, in dwords (16-by
 }  // namespace
 
 template <class F, typename YT>
-__global__ __launch_bounds__(256) void k_gemv_t(QArgs a, const f16* x, YT* y, int N, int cpl, int ntiles) {
+__global__ __launch_bounds__(256) void k_gemv_t(QArgs a, const f16* x, int M, YT* y, int N, int cpl, int ntiles) {
   extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
   constexpr int RW = rec_words<F>();
   const int t = threadIdx.x, wv = t >> 6, lane = t & 63;
   const int K = a.K, U = K / F::UE;
   const uint32_t rb = (uint32_t)a.rb, tb = kTileRows * rb;
-  uint32_t* xrec = (uint32_t*)sm;                                   // U records of RW dwords
-  uint8_t* tile = sm + (uint32_t)U * RW * 4u;                       // cpl * 4 KiB
+  uint32_t* xrec = (uint32_t*)sm;                                   // M x U records of RW dwords
+  uint8_t* tile = sm + (uint32_t)(M * U) * RW * 4u;                 // cpl * 4 KiB
   const __amdgpu_buffer_rsrc_t wr =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, (int)((uint32_t)N * rb), ALLOY_RSRC_DW3);
   const int grid = (int)gridDim.x;
@@ -59,11 +62,12 @@ __global__ __launch_bounds__(256) void k_gemv_t(QArgs a, const f16* x, YT* y, in
       }
   };
   load_tile(tl);
-  for (int u = t; u < U; u += 256) {
+  for (int i = t; i < M * U; i += 256) {
+    const int m = i / U, u = i - m * U;
     uint32_t xp[F::UE / 2];
     float xg[F::UE / 16];
-    load_x_unit<F, f16>(x, u, xp, xg);
-    uint32_t* r = xrec + u * RW;
+    load_x_unit<F, f16>(x + (size_t)m * K, u, xp, xg);
+    uint32_t* r = xrec + i * RW;
 #pragma unroll
     for (int i = 0; i < F::UE / 2; i += 4) *(u32x4*)(r + i) = u32x4{xp[i], xp[i + 1], xp[i + 2], xp[i + 3]};
     float g4[4] = {0.f, 0.f, 0.f, 0.f};
@@ -77,7 +81,7 @@ __global__ __launch_bounds__(256) void k_gemv_t(QArgs a, const f16* x, YT* y, in
 
   constexpr uint32_t esz = sizeof(YT);
   const __amdgpu_buffer_rsrc_t yr =
-      __builtin_amdgcn_make_buffer_rsrc((void*)y, (short)0, (int)((uint32_t)N * esz), ALLOY_RSRC_DW3);
+      __builtin_amdgcn_make_buffer_rsrc((void*)y, (short)0, (int)((uint32_t)(M * N) * esz), ALLOY_RSRC_DW3);
   for (; tl < ntiles; tl += grid) {
 #pragma unroll
     for (int c = 0; c < kMaxCpl; ++c)
@@ -89,31 +93,35 @@ __global__ __launch_bounds__(256) void k_gemv_t(QArgs a, const f16* x, YT* y, in
     lgkm_wait0();
     wg_barrier();
     const uint8_t* row = tile + (uint32_t)wv * rb;
-    float acc = 0.f;
-    for (int u = lane; u < U; u += 64) {
-      const uint32_t* r = xrec + u * RW;
-      uint32_t xp[F::UE / 2];
-      float xg[F::UE / 16];
-#pragma unroll
-      for (int i = 0; i < F::UE / 2; i += 4) {
-        const u32x4 q = *(const u32x4*)(r + i);
-        xp[i] = q.x; xp[i + 1] = q.y; xp[i + 2] = q.z; xp[i + 3] = q.w;
-      }
-      const u32x4 g = *(const u32x4*)(r + F::UE / 2);
-      // elements copied to scalars first: a bit_cast applied to a vector element
-      // directly picks element 0 in this compiler
-      const uint32_t g0 = g.x, g1 = g.y, g2 = g.z, g3 = g.w;
-      const float gg[4] = {__builtin_bit_cast(float, g0), __builtin_bit_cast(float, g1),
-                           __builtin_bit_cast(float, g2), __builtin_bit_cast(float, g3)};
-#pragma unroll
-      for (int i = 0; i < F::UE / 16; ++i) xg[i] = gg[i];
-      acc += F::dot(F::load_row(row, u), u, xp, xg);
-    }
-    acc = dpp_sum_rows(acc, 6);
     const uint32_t n = (uint32_t)tl * kTileRows + (uint32_t)wv;
-    const uint32_t yo = lane == 63 && n < (uint32_t)N ? n * esz : 0x80000000u;
-    if constexpr (sizeof(YT) == 4) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc), yr, yo, 0, 0);
-    else __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (f16)acc), yr, yo, 0, 0);
+    // token by token: the row's units are decoded again per token from LDS (the
+    // tile is read once from HBM whatever M is)
+    for (int m = 0; m < M; ++m) {
+      float acc = 0.f;
+      for (int u = lane; u < U; u += 64) {
+        const uint32_t* r = xrec + (m * U + u) * RW;
+        uint32_t xp[F::UE / 2];
+        float xg[F::UE / 16];
+#pragma unroll
+        for (int i = 0; i < F::UE / 2; i += 4) {
+          const u32x4 q = *(const u32x4*)(r + i);
+          xp[i] = q.x; xp[i + 1] = q.y; xp[i + 2] = q.z; xp[i + 3] = q.w;
+        }
+        const u32x4 g = *(const u32x4*)(r + F::UE / 2);
+        // elements copied to scalars first: a bit_cast applied to a vector element
+        // directly picks element 0 in this compiler
+        const uint32_t g0 = g.x, g1 = g.y, g2 = g.z, g3 = g.w;
+        const float gg[4] = {__builtin_bit_cast(float, g0), __builtin_bit_cast(float, g1),
+                             __builtin_bit_cast(float, g2), __builtin_bit_cast(float, g3)};
+#pragma unroll
+        for (int i = 0; i < F::UE / 16; ++i) xg[i] = gg[i];
+        acc += F::dot(F::load_row(row, u), u, xp, xg);
+      }
+      acc = dpp_sum_rows(acc, 6);
+      const uint32_t yo = lane == 63 && n < (uint32_t)N ? ((uint32_t)m * (uint32_t)N + n) * esz : 0x80000000u;
+      if constexpr (sizeof(YT) == 4) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc), yr, yo, 0, 0);
+      else __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (f16)acc), yr, yo, 0, 0);
+    }
     wg_barrier();                         // every wave is done with the tile in LDS
   }
 }
@@ -132,7 +140,7 @@ int tile_resident_per_cu(Kern kern, size_t lds) {
 }
 
 template <class F>
-hipError_t run_tile(const QArgs& a, const void* x, void* y, bool y_f32, int64_t N64, const Opts& o,
+hipError_t run_tile(const QArgs& a, const void* x, void* y, bool y_f32, int64_t M, int64_t N64, const Opts& o,
                     hipStream_t st) {
   static_assert(F::UE / 16 <= 4, "packed x record holds at most four sums");
   const int64_t tb = (int64_t)kTileRows * a.rb;
@@ -140,7 +148,8 @@ hipError_t run_tile(const QArgs& a, const void* x, void* y, bool y_f32, int64_t 
   if ((uint64_t)N64 * (uint64_t)a.rb >= (1ull << 31) - (1u << 20)) return hipErrorNotSupported;
   const int cpl = (int)((tb + 4095) / 4096);
   const int U = a.K / F::UE;
-  const size_t lds = (size_t)U * rec_words<F>() * 4 + (size_t)cpl * 4096;
+  if ((uint64_t)M * (uint64_t)N64 * 4u >= (1ull << 31)) return hipErrorNotSupported;
+  const size_t lds = (size_t)M * U * rec_words<F>() * 4 + (size_t)cpl * 4096;
   if (cpl > kMaxCpl || lds > 160 * 1024) return hipErrorNotSupported;
   const int N = (int)N64;
   const int ntiles = (N + kTileRows - 1) / kTileRows;
@@ -149,11 +158,11 @@ hipError_t run_tile(const QArgs& a, const void* x, void* y, bool y_f32, int64_t 
   if (o.grid_cap > 0 && o.grid_cap < grid) grid = o.grid_cap;
   if (grid > ntiles) grid = ntiles;
   if (y_f32)
-    hipLaunchKernelGGL((k_gemv_t<F, float>), dim3((unsigned)grid), dim3(256), lds, st, a, (const f16*)x, (float*)y, N,
-                       cpl, ntiles);
+    hipLaunchKernelGGL((k_gemv_t<F, float>), dim3((unsigned)grid), dim3(256), lds, st, a, (const f16*)x, (int)M,
+                       (float*)y, N, cpl, ntiles);
   else
-    hipLaunchKernelGGL((k_gemv_t<F, f16>), dim3((unsigned)grid), dim3(256), lds, st, a, (const f16*)x, (f16*)y, N,
-                       cpl, ntiles);
+    hipLaunchKernelGGL((k_gemv_t<F, f16>), dim3((unsigned)grid), dim3(256), lds, st, a, (const f16*)x, (int)M,
+                       (f16*)y, N, cpl, ntiles);
   return hipGetLastError();
 }
 
@@ -161,13 +170,13 @@ hipError_t run_tile(const QArgs& a, const void* x, void* y, bool y_f32, int64_t 
 
 hipError_t launch_gemv_tile(int fmt, const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32, int64_t M,
                             int64_t N, const Opts& o, hipStream_t st) {
-  if (M != 1 || x_f32) return hipErrorNotSupported;
+  if (M < 1 || M > kMaxTokens || x_f32) return hipErrorNotSupported;
   if (N == 0) return hipSuccess;
   switch (fmt) {
-    case F_Q6_K: return run_tile<FQ6K>(a, x, y, y_f32, N, o, st);
-    case F_Q5_0: return run_tile<FQ50>(a, x, y, y_f32, N, o, st);
-    case F_Q8_0: return run_tile<FQ80>(a, x, y, y_f32, N, o, st);
-    case F_Q4_K: return run_tile<FQ4K>(a, x, y, y_f32, N, o, st);
+    case F_Q6_K: return run_tile<FQ6K>(a, x, y, y_f32, M, N, o, st);
+    case F_Q5_0: return run_tile<FQ50>(a, x, y, y_f32, M, N, o, st);
+    case F_Q8_0: return run_tile<FQ80>(a, x, y, y_f32, M, N, o, st);
+    case F_Q4_K: return run_tile<FQ4K>(a, x, y, y_f32, M, N, o, st);
     default: return hipErrorNotSupported;
   }
 }

@@ -108,20 +108,24 @@ def test_gemv_dot2_m1(dev, fmt, N, K):
 
 
 @pytest.mark.parametrize("fmt", ["q6_k", "q5_0", "q8_0", "q4_k"])
-@pytest.mark.parametrize("N,K", [(1, 512), (37, 512), (1001, 4096), (77, 14336), (4099, 2048), (9, 1024)])
-def test_gemv_tile_staged(dev, fmt, N, K):
-    """The LDS-staged M=1 kernel (variant 4): partial last tiles, one row, the largest
-    tiles; shapes it does not take (tiles over 48 KiB) run the default kernels."""
-    rng = np.random.default_rng(N * 7 + K)
+@pytest.mark.parametrize("M,N,K", [(1, 1, 512), (3, 37, 512), (1, 1001, 4096), (2, 77, 14336), (8, 4099, 2048),
+                                   (5, 9, 1024), (2, 1024, 4096)])
+def test_gemv_tile_staged(dev, fmt, M, N, K):
+    """The LDS-staged kernel (GEMV variant 4, up to 8 activation rows): partial last
+    tiles, one row, the largest tiles; shapes it does not take (tiles over 48 KiB,
+    records over the LDS) run the default kernels."""
+    rng = np.random.default_rng(N * 7 + K + M)
     wt = Weight(fmt, N, K, rng, dev)
-    x = synth.numpy_x(1, K, rng)
+    x = synth.numpy_x(M, K, rng)
     xt = torch.from_numpy(x).to(dev)
     for od in (torch.float32, torch.float16):
         y = wt.qmm(xt, path="gemv", out_dtype=od, opts=4 << 36).float().cpu().numpy()
-        check(y, x, wt.W, f"{fmt} tile-staged gemv N={N} K={K} {od}")
-    if fmt == "q6_k":                       # the default route for Q6_K at M = 1
-        y = wt.qmm(xt, out_dtype=torch.float32).cpu().numpy()
-        check(y, x, wt.W, f"{fmt} default gemv N={N} K={K}")
+        check(y, x, wt.W, f"{fmt} tile-staged gemv M={M} N={N} K={K} {od}")
+    # the default route (the tile kernel for Q6_K at M = 1 and for small M on few rows)
+    y = wt.qmm(xt, out_dtype=torch.float32).cpu().numpy()
+    check(y, x, wt.W, f"{fmt} default route M={M} N={N} K={K}")
+    y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=9 << 36).cpu().numpy()
+    check(y, x, wt.W, f"{fmt} tile via the MFMA-path variant M={M} N={N} K={K}")
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
