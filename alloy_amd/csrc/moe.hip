@@ -53,7 +53,27 @@ MoeLayout moe_layout(int64_t T, int E, int top_k, int64_t H, int64_t I) {
 // ------------------------------------------------------------------ router
 // One wave routes token t: top-k of the E logits (ties -> lowest index, NaN never
 // wins over a number), then the softmax over the k picks in pick order.  Pick k's
-// value and index end in lane k; lane 0 writes idx / wts (and ridx, when given).
+// value and index end in lane k; lanes < k write idx / wts (and ridx, when given).
+// Each pick is a wave arg-max under the total order (value desc, index asc) by DPP
+// row operations (quad swaps, row mirrors, row broadcasts) ending in lane 63, then
+// read back as a uniform value — no LDS round trips.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void argmax_dpp(float& bv, int& bi) {
+  const int vb = __builtin_bit_cast(int, bv);
+  const float ov = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(vb, vb, CTRL, ROW_MASK, 0xF, false));
+  const int oi = __builtin_amdgcn_update_dpp(bi, bi, CTRL, ROW_MASK, 0xF, false);
+  if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+}
+__device__ __forceinline__ void wave_argmax(float& bv, int& bi) {
+  argmax_dpp<0xB1, 0xF>(bv, bi);    // quad_perm [1,0,3,2]
+  argmax_dpp<0x4E, 0xF>(bv, bi);    // quad_perm [2,3,0,1]
+  argmax_dpp<0x141, 0xF>(bv, bi);   // row_half_mirror
+  argmax_dpp<0x140, 0xF>(bv, bi);   // row_mirror: every lane holds its row's best
+  argmax_dpp<0x142, 0xA>(bv, bi);   // row_bcast:15 -> rows 1, 3
+  argmax_dpp<0x143, 0xC>(bv, bi);   // row_bcast:31 -> rows 2, 3; lane 63 holds the best
+  bv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bv), 63));
+  bi = __builtin_amdgcn_readlane(bi, 63);
+}
 template <int VPL>
 __device__ __forceinline__ void route_token(const float* logits, int64_t t, int E, int top_k,
                                             int32_t* idx, float* wts, int* ridx) {
@@ -82,18 +102,14 @@ __device__ __forceinline__ void route_token(const float* logits, int64_t t, int 
       const int e = lane + 64 * j;
       if (!((used >> j) & 1u) && (v[j] > bv || (v[j] == bv && e < bi))) { bv = v[j]; bi = e; }
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 64);
-      const int oi = __shfl_xor(bi, off, 64);
-      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
+    wave_argmax(bv, bi);
     if ((bi & 63) == lane) used |= 1u << (bi >> 6);
     if (lane == k) { myv = bv; myi = bi; }
   }
-  const float m0 = __shfl(myv, 0, 64);
+  const float m0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, myv), 0));
   float sum = 0.f;
-  for (int k = 0; k < top_k; ++k) sum += expf(__shfl(myv, k, 64) - m0);   // pick order
+  for (int k = 0; k < top_k; ++k)   // pick order
+    sum += expf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, myv), k)) - m0);
   if (lane < top_k) {
     idx[t * top_k + lane] = myi;
     wts[t * top_k + lane] = expf(myv - m0) / sum;
@@ -244,6 +260,52 @@ __global__ __launch_bounds__(1024) void k_route_sort(const float* logits, int64_
   for (int64_t t = threadIdx.x >> 6; t < T; t += kSortWaves) route_token<VPL>(logits, t, E, top_k, idx, wts, ridx);
   __syncthreads();
   sort_routes(ridx, R, E, top_k, lds + ((R + 63) & ~63), sorted, inv, tiles, ntiles);
+}
+
+// Router and sort for at most 64 routes of at most 16 tokens (every expert then has
+// at most 16 routes, one column tile): wave w routes token w, then wave 0 sorts with
+// one route per lane — rank = routes of smaller experts plus earlier routes of the
+// same expert, tile = distinct smaller experts — by a loop over the routes' experts
+// read back with readlane.  Same outputs as route + sort_routes.
+template <int VPL>
+__global__ __launch_bounds__(1024) void k_route_sort_small(const float* logits, int64_t T, int E, int top_k,
+                                                           int32_t* idx, float* wts, int32_t* sorted, int32_t* inv,
+                                                           int32_t* tiles, int32_t* ntiles) {
+  __shared__ int ridx[64];
+  const int R = (int)T * top_k;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (wave < T) route_token<VPL>(logits, wave, E, top_k, idx, wts, ridx);
+  __syncthreads();
+  if (wave != 0) return;
+  const bool valid = lane < R;
+  const int e = valid ? ridx[lane] : 0x7FFFFFFF;
+  int off = 0, cnt = 0, dup = 0;
+  for (int j = 0; j < R; ++j) {
+    const int ej = __builtin_amdgcn_readlane(e, j);
+    off += ej < e ? 1 : 0;                    // routes of smaller experts
+    cnt += ej == e ? 1 : 0;
+    dup += (ej == e && j < lane) ? 1 : 0;     // earlier routes of the same expert
+  }
+  const int rank = off + dup, first = dup == 0 ? 1 : 0;   // first: its expert's first route
+  int tile = 0, nd = 0;
+  for (int j = 0; j < R; ++j) {
+    const int fj = __builtin_amdgcn_readlane(first, j);
+    tile += (fj && __builtin_amdgcn_readlane(e, j) < e) ? 1 : 0;   // distinct smaller experts
+    nd += fj;
+  }
+  if (valid) {
+    sorted[rank] = lane;
+    inv[lane] = rank;
+    int32_t* tp = tiles + kTileInts * tile;
+    tp[4 + (rank - off)] = lane / top_k;
+    if (dup == 0) {
+      tp[0] = e;
+      tp[1] = off;
+      tp[2] = cnt;
+      tp[3] = 0;
+    }
+  }
+  if (lane == 0) *ntiles = nd;
 }
 
 // ------------------------------------------------------------------ grouped GEMVs
@@ -461,6 +523,19 @@ static hipError_t route_and_sort(const MoeArgs& m, const MoeLayout& L, hipStream
   int32_t* ntiles = (int32_t*)(m.ws + L.ntiles);
   hipError_t e = hipSuccess;
   const size_t sort_lds = (size_t)(kSortWaves * m.E + 2 * m.E + 64) * sizeof(int);
+  if (L.R <= 64 && m.T <= kMoeColTile) {
+    const int vpl = (m.E + 63) / 64;
+    const dim3 g(1), b((unsigned)(64 * m.T));
+    if (vpl <= 2)
+      hipLaunchKernelGGL(k_route_sort_small<2>, g, b, 0, st, m.logits, m.T, m.E, m.top_k, idx, wts, sorted, inv, tiles, ntiles);
+    else if (vpl <= 4)
+      hipLaunchKernelGGL(k_route_sort_small<4>, g, b, 0, st, m.logits, m.T, m.E, m.top_k, idx, wts, sorted, inv, tiles, ntiles);
+    else if (vpl <= 8)
+      hipLaunchKernelGGL(k_route_sort_small<8>, g, b, 0, st, m.logits, m.T, m.E, m.top_k, idx, wts, sorted, inv, tiles, ntiles);
+    else
+      hipLaunchKernelGGL(k_route_sort_small<16>, g, b, 0, st, m.logits, m.T, m.E, m.top_k, idx, wts, sorted, inv, tiles, ntiles);
+    return hipGetLastError();
+  }
   if (m.T <= kFusedTokens) {
     const size_t shm = sort_lds + (size_t)((L.R + 63) & ~63) * sizeof(int);
     auto fused = [&](auto kern) -> hipError_t {
