@@ -174,13 +174,6 @@ __global__ __launch_bounds__(256) void k_gemv_dot2(QArgs a, const XT* x, void* y
 }
 
 // ------------------------------------------------------------------ M=1 GEMV, wave rows
-// Formats whose wave-path raw loads are completed across lanes before the dot
-// (F::share), e.g. a header loaded a dword per lane.
-template <class F, class = void>
-struct HasShare : std::false_type {};
-template <class F>
-struct HasShare<F, std::void_t<decltype(F::share(std::declval<typename F::Raw&>()))>> : std::true_type {};
-
 // L = 16, 32 or 64 lanes share a row inside one wave (64/L rows per wave, 256/L per
 // workgroup); each lane owns UPT decode units of the row, the same for every row
 // it visits, with their x in registers.  Weights stream through a ring of D rows

@@ -2,9 +2,19 @@
 // pair order, the DPP row reductions, a fence-free workgroup barrier, and the
 // v_fma_mix dequant steps of the Q4_K GEMMs.
 #pragma once
+#include <type_traits>
+#include <utility>
+
 #include "qformats.h"
 
 namespace alloy {
+
+// Formats whose wave-path raw loads are completed across lanes before the dot
+// (F::share), e.g. a header loaded a dword per lane.
+template <class F, class = void>
+struct HasShare : std::false_type {};
+template <class F>
+struct HasShare<F, std::void_t<decltype(F::share(std::declval<typename F::Raw&>()))>> : std::true_type {};
 
 // Compiler-opaque workgroup barrier and LDS wait: no fence, so loads still in flight
 // (a GEMV's weight prefetch) are not drained at the barrier; the memory clobber

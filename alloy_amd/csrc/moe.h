@@ -20,7 +20,8 @@ struct MoeLayout {
   size_t inv = 0;         // i32[R]   route -> expert-sorted position
   size_t tiles = 0;       // i32[max_tiles][4]: expert, first sorted position, count, pad
   size_t ntiles = 0;      // i32[1]   number of valid tiles
-  size_t h = 0;           // f32[R][I]  silu(gate) * up per sorted position
+  size_t h = 0;           // f32[R][I]  silu(gate) * up per sorted position (xs path);
+                          // f32[R][2I] gate | up per route (routed wave path)
   size_t part = 0;        // f32[R][H]  down projection per sorted position
   size_t total = 0;
 };

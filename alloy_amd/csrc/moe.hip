@@ -26,6 +26,7 @@
 //   5. k_combine    y[t] = sum_s w[t,s] * partial[inv[t,s]] in slot order
 //                   (reference role: moe.py:479-501, fixed-order combine)
 // Each expert's weights are read once per column tile of its routed tokens.
+#include "gemv.h"
 #include "moe.h"
 #include "xs.h"
 
@@ -44,7 +45,7 @@ MoeLayout moe_layout(int64_t T, int E, int top_k, int64_t H, int64_t I) {
   L.inv = o; o = align256(o + 4 * (size_t)L.R);
   L.tiles = o; o = align256(o + 4 * kTileInts * (size_t)L.max_tiles);
   L.ntiles = o; o = align256(o + 4);
-  L.h = o; o = align256(o + 4 * (size_t)L.R * (size_t)I);
+  L.h = o; o = align256(o + 8 * (size_t)L.R * (size_t)I);   // f32[R][I] (f32[R][2I] routed path)
   L.part = o; o = align256(o + 4 * (size_t)L.R * (size_t)H);
   L.total = o;
   return L;
@@ -111,8 +112,8 @@ __device__ __forceinline__ void route_token(const float* logits, int64_t t, int 
   for (int k = 0; k < top_k; ++k)   // pick order
     sum += expf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, myv), k)) - m0);
   if (lane < top_k) {
-    idx[t * top_k + lane] = myi;
-    wts[t * top_k + lane] = expf(myv - m0) / sum;
+    if (idx) idx[t * top_k + lane] = myi;
+    if (wts) wts[t * top_k + lane] = expf(myv - m0) / sum;
     if (ridx) ridx[t * top_k + lane] = myi;
   }
 }
@@ -456,7 +457,7 @@ __global__ __launch_bounds__(256) void k_combine(const float* part, const int32_
   float acc = 0.f;
   for (int s = 0; s < top_k; ++s) {
     const int64_t r = t * top_k + s;
-    acc += wts[r] * part[(int64_t)inv[r] * H + j];
+    acc += wts[r] * part[(int64_t)(inv ? inv[r] : r) * H + j];   // no inv: partials in route order
   }
   y[t * H + j] = acc;
 }
@@ -569,7 +570,225 @@ static hipError_t combine(const MoeArgs& m, const MoeLayout& L, hipStream_t st) 
   return hipGetLastError();
 }
 
+// ------------------------------------------------------------------ routed wave GEMV (few tokens)
+// For T <= kRoutedTokens each route slot r (token r / top_k, expert idx[r]) is one
+// GEMV over its expert's rows, on the lane / unit layout of the dense wave-row GEMV
+// (k_gemv_w): L lanes per row, <= 4 units per lane with their x in registers, a
+// one-row register ring of weights, DPP row sums.  The workgroup's expert is read on
+// the device (blockIdx.x = slot * gx + row group).  MODE 0 (gate/up): x = the slot's
+// token row, y = fp32 rows [0, 2I) of the slot.  MODE 1 (down): x = silu(g) * u of
+// the slot's fp32 gate/up row, scaled by a power of two so its largest magnitude lands
+// in [2^14, 2^15) before the fp16 rounding; the sums are scaled back on the store.
+constexpr int kRoutedTokens = 16;
+
+template <class F, int UPT, int MODE, int VPL>
+__global__ __launch_bounds__(256) void k_gemv_routed(QArgs a, uint32_t sb, int32_t* idx, float* wts,
+                                                     const float* logits, int E, int top_k, const void* xsrc, int N,
+                                                     float* ys, int gx, int lshift) {
+  const int r = (int)blockIdx.x / gx, bx = (int)blockIdx.x - r * gx;
+  int e;
+  if constexpr (VPL > 0) {
+    // the router runs here (wave 0 routes the slot's token; the token's first
+    // workgroup stores idx / wts for the later launches): no separate launch
+    __shared__ int picks[64];
+    const int tk = r / top_k;
+    if (threadIdx.x < 64) {
+      const bool store = bx == 0 && r % top_k == 0;
+      route_token<VPL>(logits + (int64_t)tk * E, 0, E, top_k, store ? idx + tk * top_k : nullptr,
+                       store ? wts + tk * top_k : nullptr, picks);
+    }
+    __syncthreads();
+    e = __builtin_amdgcn_readfirstlane(picks[r % top_k]);
+  } else {
+    e = __builtin_amdgcn_readfirstlane(idx[r]);
+  }
+  const int64_t row0 = (int64_t)e * N;               // the expert's first row
+  a.w += row0 * a.rb;
+  if (a.s) a.s += row0 * (sb / 2);
+  if (a.b) a.b += row0 * (sb / 2);
+  const int L = 1 << lshift;
+  const int t = threadIdx.x, li = t & (L - 1), slot = t >> lshift;
+  const int R = blockDim.x >> lshift;
+  const int K = a.K, U = K / F::UE;
+  const uint32_t rb = (uint32_t)a.rb;
+  const Src src(a, (uint32_t)N * rb, (uint32_t)N * sb);
+  const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(ys + (int64_t)r * N), (short)0, (int)((uint32_t)N * 4u), ALLOY_RSRC_DW3);
+  bool own[UPT];
+  int uu[UPT];
+  uint32_t wo[UPT], so[UPT];
+#pragma unroll
+  for (int j = 0; j < UPT; ++j) {
+    const int u = li + L * j;
+    own[j] = u < U;
+    uu[j] = own[j] ? u : U - 1;
+    wo[j] = own[j] ? F::woff(a, uu[j]) : 0x80000000u;
+    so[j] = own[j] ? F::soff(a, uu[j]) : 0x80000000u;
+  }
+  const int stride = gx * R;
+  const int n0 = bx * R + slot;
+  uint32_t rw = (uint32_t)n0 * rb, rs = (uint32_t)n0 * sb;
+  const uint32_t dw = (uint32_t)stride * rb, ds = (uint32_t)stride * sb;
+
+  constexpr int XV = 512 * F::UE / 4096;             // 16-byte chunks per thread at the largest K
+  __shared__ __attribute__((aligned(16))) f16 xl[256 * F::UE];
+  __shared__ float wmax[4];
+  float yscale = 1.f;
+  u32x4 xv[XV], uv[XV];
+  const uint32_t xbytes = (MODE == 0 ? 2u : 4u) * (uint32_t)K;   // one activation / gate row
+  if constexpr (MODE == 0) {
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)((const f16*)xsrc + (int64_t)(r / top_k) * K), (short)0, (int)xbytes, ALLOY_RSRC_DW3);
+#pragma unroll
+    for (int i = 0; i < XV; ++i)
+      if (4096u * i < xbytes) xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (uint32_t)t * 16u + 4096u * i, 0, 0);
+  } else {
+    // gate and up rows of the slot (fp32, K each); thread t holds elements 4t + 1024i
+    const float* gu = (const float*)xsrc + (int64_t)r * 2 * K;
+    const __amdgpu_buffer_rsrc_t grs = __builtin_amdgcn_make_buffer_rsrc((void*)gu, (short)0, (int)xbytes, ALLOY_RSRC_DW3);
+    const __amdgpu_buffer_rsrc_t urs = __builtin_amdgcn_make_buffer_rsrc((void*)(gu + K), (short)0, (int)xbytes, ALLOY_RSRC_DW3);
+#pragma unroll
+    for (int i = 0; i < XV; ++i)
+      if (4096u * i < xbytes) {
+        xv[i] = __builtin_amdgcn_raw_buffer_load_b128(grs, (uint32_t)t * 16u + 4096u * i, 0, 0);
+        uv[i] = __builtin_amdgcn_raw_buffer_load_b128(urs, (uint32_t)t * 16u + 4096u * i, 0, 0);
+      }
+  }
+  typename F::Raw ring[UPT];
+#pragma unroll
+  for (int j = 0; j < UPT; ++j) ring[j] = F::load_b(src, rw + wo[j], rs + so[j], uu[j]);
+  if constexpr (MODE == 0) {
+#pragma unroll
+    for (int i = 0; i < XV; ++i)
+      if (4096u * i < xbytes) *(u32x4*)((uint8_t*)xl + t * 16 + 4096 * i) = xv[i];
+  } else {
+    float hv[XV][4];
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+      const uint32_t g0 = xv[i].x, g1 = xv[i].y, g2 = xv[i].z, g3 = xv[i].w;   // scalars first
+      const uint32_t u0 = uv[i].x, u1 = uv[i].y, u2 = uv[i].z, u3 = uv[i].w;
+      const uint32_t gb[4] = {g0, g1, g2, g3}, ub[4] = {u0, u1, u2, u3};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float g = __builtin_bit_cast(float, gb[q]), u = __builtin_bit_cast(float, ub[q]);
+        const float h = g / (1.f + __expf(-g)) * u;
+        hv[i][q] = h;
+        mx = fmaxf(mx, fabsf(h));
+      }
+    }
+    // workgroup max |h| (fixed-shape reduction; max is order independent)
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    if ((t & 63) == 0) wmax[t >> 6] = mx;
+    lgkm_wait0();
+    wg_barrier();
+    mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    int ex = 0;
+    (void)frexpf(mx, &ex);                              // mx = f * 2^ex, f in [0.5, 1)
+    const float xs = (mx > 0.f && mx < INFINITY) ? ldexpf(1.f, 15 - ex) : 1.f;
+    yscale = 1.f / xs;                                  // exact: a power of two
+#pragma unroll
+    for (int i = 0; i < XV; ++i)
+      if (4096u * i < xbytes) {
+        const f16x4 hh = f16x4{(f16)(hv[i][0] * xs), (f16)(hv[i][1] * xs), (f16)(hv[i][2] * xs), (f16)(hv[i][3] * xs)};
+        *(f16x4*)((uint8_t*)xl + t * 8 + 2048 * i) = hh;
+      }
+  }
+  lgkm_wait0();
+  wg_barrier();
+  uint32_t xr[UPT][F::UE / 2];
+  float xg[UPT][F::UE / 16];
+#pragma unroll
+  for (int j = 0; j < UPT; ++j) load_x_unit<F, f16>(xl, uu[j], xr[j], xg[j]);
+
+  for (int nb = bx * R; nb < N; nb += stride) {        // uniform across the workgroup
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < UPT; ++j) {
+      if constexpr (HasShare<F>::value) F::share(ring[j]);
+      const float v = F::dot(ring[j], uu[j], xr[j], xg[j]);
+      acc += own[j] ? v : 0.f;
+    }
+    rw += dw;
+    rs += ds;
+#pragma unroll
+    for (int j = 0; j < UPT; ++j) ring[j] = F::load_b(src, rw + wo[j], rs + so[j], uu[j]);
+    acc = dpp_sum_rows(acc, lshift) * yscale;
+    const uint32_t yo = li == L - 1 ? (uint32_t)(nb + slot) * 4u : 0x80000000u;
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc), yr, yo, 0, 0);
+  }
+}
+
+template <class F, int MODE>
+static hipError_t launch_routed(const QArgs& a, uint32_t sb, int32_t* idx, float* wts, const float* logits, int E,
+                                int top_k, const void* xsrc, int N, float* ys, int64_t R, hipStream_t st) {
+  const int U = a.K / F::UE;
+  if (a.K % 256 || U > 256 || (MODE == 1 && a.K > 4096)) return hipErrorNotSupported;
+  int lshift = U <= 64 ? 4 : U <= 128 ? 5 : 6;
+  const int cus = xs_cu_count();
+  while (lshift < 6 && R * ((int64_t)N << lshift) < (int64_t)2 * cus * 256) ++lshift;   // enough workgroups
+  const int L = 1 << lshift, upt = (U + L - 1) / L, rows = 256 >> lshift;
+  if (upt > 4) return hipErrorNotSupported;
+  int64_t gx = (N + rows - 1) / rows;
+  const int64_t cap = (3 * (int64_t)cus + R - 1) / R;
+  if (gx > cap) gx = cap;
+  const dim3 grid((unsigned)(R * gx)), block(256);
+  // logits given: the router is fused in (E <= 128 or <= 256 experts); else idx is read
+  const int vpl = logits ? (E <= 128 ? 2 : E <= 256 ? 4 : -1) : 0;
+  if (vpl < 0) return hipErrorNotSupported;
+  auto go = [&](auto u, auto v) {
+    constexpr int UP = decltype(u)::value, VP = decltype(v)::value;
+    hipLaunchKernelGGL((k_gemv_routed<F, UP, MODE, VP>), grid, block, 0, st, a, sb, idx, wts, logits, E, top_k, xsrc, N,
+                       ys, (int)gx, lshift);
+    return hipGetLastError();
+  };
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  using I4 = std::integral_constant<int, 4>;
+  using V0 = std::integral_constant<int, 0>;
+  if constexpr (MODE == 0) {
+    if (vpl == 2) return upt == 1 ? go(I1(), I2()) : upt == 2 ? go(I2(), I2()) : upt == 3 ? go(I3(), I2()) : go(I4(), I2());
+    if (vpl == 4) return upt == 1 ? go(I1(), I4()) : upt == 2 ? go(I2(), I4()) : upt == 3 ? go(I3(), I4()) : go(I4(), I4());
+  }
+  return upt == 1 ? go(I1(), V0()) : upt == 2 ? go(I2(), V0()) : upt == 3 ? go(I3(), V0()) : go(I4(), V0());
+}
+
+// Few tokens: gate/up with the router fused in (2I rows of each slot's expert), down
+// (H rows over silu(g)*u), combine over the slots in route order: three launches.
+template <class FG, class FD>
+static hipError_t routed_moe(const MoeArgs& m, const MoeLayout& L, uint32_t sbg, uint32_t sbd, hipStream_t st) {
+  int32_t* idx = (int32_t*)(m.ws + L.idx);
+  float* wts = (float*)(m.ws + L.wts);
+  float* gu = (float*)(m.ws + L.h);
+  float* part = (float*)(m.ws + L.part);
+  hipError_t e = launch_routed<FG, 0>(m.gu, sbg, idx, wts, m.logits, m.E, m.top_k, m.x, (int)(2 * m.I), gu, L.R, st);
+  if (e == hipErrorNotSupported) {            // many experts: a separate router launch
+    (void)hipGetLastError();
+    if ((e = launch_router(m.logits, idx, wts, m.T, m.E, m.top_k, st)) != hipSuccess) return e;
+    e = launch_routed<FG, 0>(m.gu, sbg, idx, wts, nullptr, m.E, m.top_k, m.x, (int)(2 * m.I), gu, L.R, st);
+  }
+  if (e != hipSuccess) return e;
+  if ((e = launch_routed<FD, 1>(m.dn, sbd, idx, wts, nullptr, m.E, m.top_k, gu, (int)m.H, part, L.R, st)) != hipSuccess)
+    return e;
+  hipLaunchKernelGGL(k_combine, dim3((unsigned)m.T, (unsigned)((m.H + 255) / 256)), dim3(256), 0, st,
+                     (const float*)part, (const int32_t*)nullptr, (const float*)wts, m.y, m.top_k, (int)m.H);
+  return hipGetLastError();
+}
+
+static bool routed_fits(const MoeArgs& m) {
+  // 32-bit offsets within one expert; gate/up K = H and down K = I multiples of 256
+  return m.T <= kRoutedTokens && m.H % 256 == 0 && m.I % 256 == 0 && m.H <= 8192 && m.I <= 4096 &&
+         (uint64_t)(2 * m.I + 256) * (uint64_t)m.gu.rb < (1ull << 31) && (uint64_t)(m.H + 256) * (uint64_t)m.dn.rb < (1ull << 31);
+}
+
 hipError_t launch_mlx_moe(const MoeArgs& m, const MoeLayout& L, hipStream_t st) {
+  if (routed_fits(m) && m.gu.gs >= 32 && m.dn.gs >= 32) {
+    const hipError_t r = routed_moe<FMLX, FMLX>(m, L, 2u * (uint32_t)(m.H / m.gu.gs), 2u * (uint32_t)(m.I / m.dn.gs), st);
+    if (r != hipErrorNotSupported) return r;
+    (void)hipGetLastError();
+  }
   int32_t* sorted = (int32_t*)(m.ws + L.sorted);
   int32_t* tiles = (int32_t*)(m.ws + L.tiles);
   int32_t* ntiles = (int32_t*)(m.ws + L.ntiles);
@@ -602,6 +821,11 @@ bool gguf_moe_supported(int64_t T, int64_t H, int64_t I, const MoeLayout& L) {
 
 hipError_t launch_gguf_moe(const MoeArgs& m, const MoeLayout& L, hipStream_t st) {
   if (!gguf_moe_supported(m.T, m.H, m.I, L)) return hipErrorNotSupported;
+  if (routed_fits(m)) {
+    const hipError_t r = routed_moe<FQ4K, FQ6K>(m, L, 0u, 0u, st);
+    if (r != hipErrorNotSupported) return r;
+    (void)hipGetLastError();
+  }
   hipError_t e = route_and_sort(m, L, st);
   if (e != hipSuccess) return e;
   XsJob g{};

@@ -65,7 +65,7 @@ def run_case(dev, T, E, k, H, I, gs, seed, tokens=None):
     return y
 
 
-@pytest.mark.parametrize("T", [1, 5, 40])
+@pytest.mark.parametrize("T", [1, 2, 4, 5, 40])
 def test_moe_small(dev, T):
     run_case(dev, T, E=8, k=2, H=256, I=128, gs=64, seed=T)
 
@@ -149,7 +149,7 @@ def run_gguf_case(dev, T, E, k, H, I, seed, tokens=None, logits_dtype=torch.floa
     return y
 
 
-@pytest.mark.parametrize("T", [1, 5, 21])
+@pytest.mark.parametrize("T", [1, 2, 4, 5, 21])
 def test_gguf_moe_small(dev, T):
     # gate/up K = 512 (2 waves), down K = 256 (1 wave); full and partial tiles
     run_gguf_case(dev, T, E=8, k=2, H=512, I=256, seed=50 + T)
