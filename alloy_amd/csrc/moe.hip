@@ -666,6 +666,7 @@ __global__ __launch_bounds__(256) void k_gemv_routed(QArgs a, uint32_t sb, int32
     float mx = 0.f;
 #pragma unroll
     for (int i = 0; i < XV; ++i) {
+      if (4096u * i >= xbytes) break;                   // chunks past the row were not loaded
       const uint32_t g0 = xv[i].x, g1 = xv[i].y, g2 = xv[i].z, g3 = xv[i].w;   // scalars first
       const uint32_t u0 = uv[i].x, u1 = uv[i].y, u2 = uv[i].z, u3 = uv[i].w;
       const uint32_t gb[4] = {g0, g1, g2, g3}, ub[4] = {u0, u1, u2, u3};

@@ -26,10 +26,10 @@ def to_dev(arrs, shape_q, shape_s, dev):
             torch.from_numpy(b).reshape(shape_s).to(dev))
 
 
-def run_case(dev, T, E, k, H, I, gs, seed, tokens=None):
+def run_case(dev, T, E, k, H, I, gs, seed, tokens=None, x_scale=1.0):
     rng = np.random.default_rng(seed)
     gu, dn = make_experts(E, H, I, gs, rng)
-    x = synth.numpy_x(T, H, rng)
+    x = (synth.numpy_x(T, H, rng).astype(np.float32) * x_scale).astype(np.float16)
     logits = rng.standard_normal((T, E)).astype(np.float32)
     guq, gus, gub = to_dev(gu, (E, 2 * I, H // 2), (E, 2 * I, H // gs), dev)
     dnq, dns, dnb = to_dev(dn, (E, H, I // 2), (E, H, I // gs), dev)
@@ -68,6 +68,16 @@ def run_case(dev, T, E, k, H, I, gs, seed, tokens=None):
 @pytest.mark.parametrize("T", [1, 2, 4, 5, 40])
 def test_moe_small(dev, T):
     run_case(dev, T, E=8, k=2, H=256, I=128, gs=64, seed=T)
+
+
+@pytest.mark.parametrize("E,k,T,x_scale", [(8, 4, 3, 1.0), (200, 4, 3, 1.0), (300, 6, 5, 1.0), (16, 2, 9, 40.0),
+                                             (16, 2, 7, 1e-3)])
+def test_moe_routed_small_t(dev, E, k, T, x_scale):
+    # few tokens with I a multiple of 256: per-route GEMVs, the router fused into gate/up
+    # (E <= 256) or a launch of its own (E = 300); experts shared by several tokens;
+    # large and tiny activations exercise the per-route power-of-two scaling of
+    # silu(g)*u before its fp16 rounding
+    run_case(dev, T, E=E, k=k, H=512, I=256, gs=64, seed=E + T, x_scale=x_scale)
 
 
 @pytest.mark.parametrize("gs", [32, 64, 128, 256])
