@@ -244,8 +244,7 @@ __global__ __launch_bounds__(256) void k_gemv_w(WaveBatchT<NB> bt, uint32_t sb, 
 #pragma unroll
   for (int i = 0; i < XV; ++i)
     if (4096u * i < xbytes) *(u32x4*)((uint8_t*)xl + t * 16 + 4096 * i) = xv[i];
-  lgkm_wait0();
-  wg_barrier();
+  lds_barrier_asm();
   uint32_t xr[UPT][F::UE / 2];
   float xg[UPT][F::UE / 16];
 #pragma unroll
@@ -1385,7 +1384,7 @@ struct GemvMfmaRun {
 // M <= 16 on the generic x-stationary kernel (Q4_K, Q6_K, MLX with a power-of-two
 // group size); hipErrorNotSupported when the format or shape does not fit it.
 static hipError_t launch_gemv_xs(int fmt, const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32,
-                                 int64_t M, int64_t N, const Opts& o, hipStream_t st) {
+                                 int64_t M, int64_t N, const Opts& o, hipStream_t st, bool dq = false) {
   if (x_f32 || M > 16 || N >= (1ll << 31) || (uint64_t)M * (uint64_t)a.K * 2u >= (1ull << 31))
     return hipErrorNotSupported;
   XsJob j{};
@@ -1398,10 +1397,28 @@ static hipError_t launch_gemv_xs(int fmt, const QArgs& a, const void* x, bool x_
   j.y = y;
   j.y_f32 = y_f32;
   const int64_t cap = o.grid_cap > 0 ? o.grid_cap : 1024;
-  if (fmt == F_Q4_K) return launch_xs<XsQ4K, 0>(j, 0, cap, o.row_groups, st);
-  if (fmt == F_Q6_K) return launch_xs<XsQ6K, 0>(j, 0, cap, o.row_groups, st);
+  if (dq) {
+    // measured on the config 2 / 3 shapes: wide matrices loop one workgroup per CU
+    // over their tiles (next tiles' weights in flight); Q4_K at M > 8 on mid-size N
+    // takes two tiles per reduction
+    const int64_t dcap = o.grid_cap > 0 ? o.grid_cap : N >= 12288 ? xs_cu_count() : 1024;
+    const int rt = o.row_groups ? o.row_groups : fmt == F_Q4_K && M > 8 && N > 4096 && N < 12288 ? 2 : 1;
+    if (fmt == F_Q4_K) return launch_xs<XsDQ<XsQ4K>, 0>(j, 0, dcap, rt, st);
+    if (fmt == F_Q6_K) return launch_xs<XsDQ<XsQ6K>, 0>(j, 0, dcap, rt, st);
+  } else {
+    if (fmt == F_Q4_K) return launch_xs<XsQ4K, 0>(j, 0, cap, o.row_groups, st);
+    if (fmt == F_Q6_K) return launch_xs<XsQ6K, 0>(j, 0, cap, o.row_groups, st);
+  }
   if (fmt != F_MLX || a.gs < 32 || (a.gs & (a.gs - 1))) return hipErrorNotSupported;
   j.sb = (uint32_t)(a.K / a.gs * 2);
+  if (dq) {
+    switch (a.gs) {
+      case 32: return launch_xs<XsDQ<XsMLX<0>>, 0>(j, 0, cap, o.row_groups, st);
+      case 64: return launch_xs<XsDQ<XsMLX<1>>, 0>(j, 0, cap, o.row_groups, st);
+      case 128: return launch_xs<XsDQ<XsMLX<2>>, 0>(j, 0, cap, o.row_groups, st);
+      default: return a.gs == 256 ? launch_xs<XsDQ<XsMLX<3>>, 0>(j, 0, cap, o.row_groups, st) : hipErrorNotSupported;
+    }
+  }
   switch (a.gs) {
     case 32: return launch_xs<XsMLX<0>, 0>(j, 0, cap, o.row_groups, st);
     case 64: return launch_xs<XsMLX<1>, 0>(j, 0, cap, o.row_groups, st);
@@ -1458,18 +1475,18 @@ hipError_t launch_glu_combine(int act, const float* g, const float* u, void* y, 
 }
 
 // Default kernel choice for 2 <= M <= 16 (measured on the config 2 / 3 shapes):
-//   Q4_K  tall (N >= 32768) and 3 <= M <= 6: 4x4x4 broadcast kernel; K > 4096: the
-//         Q4_K x-stationary kernel (its 16-slot waves beat the generic ones); else
-//         the generic x-stationary kernel
-//   Q6_K  generic x-stationary while N <= 8192, else the 16x16x32 kernel
-//   MLX   generic x-stationary
+//   Q4_K  tall (N >= 32768) and 3 <= M <= 6: 4x4x4 broadcast kernel; K <= 8192: the
+//         x-stationary kernel with fp16-dequantised weights (8); else the Q4_K
+//         x-stationary kernel
+//   Q6_K  K <= 4096: x-stationary with fp16-dequantised weights, else 16x16x32
+//   MLX   generic x-stationary (exact products; dequantising measured no faster)
 //   other formats (and shapes the above do not take): 16x16x32 kernel
 static int mfma_variant(int fmt, int64_t M, int64_t N, int64_t K) {
   if (fmt == F_Q4_K) {
     if (N >= 32768 && M >= 3 && M <= 6) return 5;
-    return K > 4096 ? 6 : 7;
+    return K <= 8192 ? 8 : 6;
   }
-  if (fmt == F_Q6_K) return N <= 8192 ? 7 : 1;
+  if (fmt == F_Q6_K) return K <= 4096 ? 8 : 1;
   if (fmt == F_MLX) return 7;
   return 1;
 }
@@ -1487,6 +1504,7 @@ hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, 
   hipError_t e = hipErrorNotSupported;
   if (v == 9) e = launch_gemv_tile(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
   else if (v == 7) e = launch_gemv_xs(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
+  else if (v == 8) e = launch_gemv_xs(fmt, a, x, x_f32, y, y_f32, M, N, o, st, true);
   else if (v == 6 && fmt == F_Q4_K) e = launch_gemv_xs_q4k(a, x, x_f32, y, y_f32, M, N, o, st);
   else if (v == 5 && fmt == F_Q4_K) e = launch_gemv_q4k_m4(a, x, x_f32, y, y_f32, M, N, o, st);
   if (e != hipErrorNotSupported) return e;

@@ -90,8 +90,7 @@ __global__ __launch_bounds__(256) void k_gemv_t(QArgs a, const f16* x, int M, YT
         if (o < tb) *(u32x4*)(tile + o) = v[c];
       }
     load_tile(tl + grid);                 // next tile in flight during this one
-    lgkm_wait0();
-    wg_barrier();
+    lds_barrier_asm();
     const uint8_t* row = tile + (uint32_t)wv * rb;
     const uint32_t n = (uint32_t)tl * kTileRows + (uint32_t)wv;
     // token by token: the row's units are decoded again per token from LDS (the
@@ -122,7 +121,7 @@ __global__ __launch_bounds__(256) void k_gemv_t(QArgs a, const f16* x, int M, YT
       if constexpr (sizeof(YT) == 4) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc), yr, yo, 0, 0);
       else __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (f16)acc), yr, yo, 0, 0);
     }
-    wg_barrier();                         // every wave is done with the tile in LDS
+    lds_barrier_asm();                    // every wave is done with the tile in LDS
   }
 }
 

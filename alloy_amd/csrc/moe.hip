@@ -682,8 +682,7 @@ __global__ __launch_bounds__(256) void k_gemv_routed(QArgs a, uint32_t sb, int32
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
     if ((t & 63) == 0) wmax[t >> 6] = mx;
-    lgkm_wait0();
-    wg_barrier();
+    lds_barrier_asm();
     mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
     int ex = 0;
     (void)frexpf(mx, &ex);                              // mx = f * 2^ex, f in [0.5, 1)
@@ -696,8 +695,7 @@ __global__ __launch_bounds__(256) void k_gemv_routed(QArgs a, uint32_t sb, int32
         *(f16x4*)((uint8_t*)xl + t * 8 + 2048 * i) = hh;
       }
   }
-  lgkm_wait0();
-  wg_barrier();
+  lds_barrier_asm();
   uint32_t xr[UPT][F::UE / 2];
   float xg[UPT][F::UE / 16];
 #pragma unroll

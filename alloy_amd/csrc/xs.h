@@ -17,6 +17,7 @@
 #pragma once
 #include <atomic>
 #include <type_traits>
+#include "gemv.h"
 #include "launch.h"
 
 namespace alloy {
@@ -73,6 +74,24 @@ __device__ __forceinline__ f32x4 xs_mfma32(f16x8 a, u32x4 b, f32x4 d) {
 }
 constexpr f16x8 kXsOnes = {1, 1, 1, 1, 1, 1, 1, 1};
 
+template <int I, int N, class Fn>
+__device__ __forceinline__ void xs_static_for(Fn&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>());
+    xs_static_for<I + 1, N>(f);
+  }
+}
+
+// Dequant of two 4/6-bit quants held as fp16 denormals (q 2^-24, the halves of `a`):
+// RN16(s * (q 2^-24) + c) for each half, with s = the weight scale times 2^24.  The
+// compiler emits this as v_fma_mixlo/hi_f16 (fp32 fma of the converted half, one
+// rounding to fp16), so each weight is the exact value rounded once.
+__device__ __forceinline__ uint32_t xs_dq2(uint32_t a, float s, float c) {
+  const f16x2 v = __builtin_bit_cast(f16x2, a);
+  const f16x2 o = {(_Float16)__builtin_fmaf(s, (float)v.x, c), (_Float16)__builtin_fmaf(s, (float)v.y, c)};
+  return __builtin_bit_cast(uint32_t, o);
+}
+
 // Q4_K: unit = one 144-byte super-block; one chain per 32-element sub-block J (one
 // 16x16x32 MFMA).  The lane reads the 16-byte header and bytes 8kq .. 8kq+7 of each
 // 32-byte quant pair p (low nibbles: sub-block 2p, high: 2p+1, as 1024 + 16q).
@@ -111,6 +130,21 @@ struct XsQ4K {
     q4k_scale_min(r.hd.y, r.hd.z, r.hd.w, C, scl, mn);
     s = h2f(r.hd.x) * (float)scl * ((C & 1) ? 0.0625f : 1.f);
     c = -(h2f(r.hd.x >> 16) * (float)mn) - 1024.f * s;
+  }
+  // chain C with the weights dequantised to fp16 (d sc q - dmin m, rounded once),
+  // accumulated into acc; nibbles masked in place (high ones as 16 q, scale / 16)
+  template <int C>
+  __device__ static void dq(const f16x8* xu, const Raw& r, f32x4& acc) {
+    constexpr int p = C >> 1;
+    constexpr uint32_t m = (C & 1) ? 0x00F000F0u : 0x000F000Fu;
+    uint32_t scl, mn;
+    q4k_scale_min(r.hd.y, r.hd.z, r.hd.w, C, scl, mn);
+    const float s = h2f(r.hd.x) * (float)scl * ((C & 1) ? 1048576.f : 16777216.f);
+    const float c = -(h2f(r.hd.x >> 16) * (float)mn);
+    const uint32_t w0 = r.q[p].x, w1 = r.q[p].y;            // pairs in the xload order
+    const u32x4 b = {xs_dq2(w0 & m, s, c), xs_dq2((w0 >> 8) & m, s, c), xs_dq2(w1 & m, s, c),
+                     xs_dq2((w1 >> 8) & m, s, c)};
+    acc = xs_mfma32(xu[C], b, acc);
   }
 };
 
@@ -195,6 +229,22 @@ struct XsMLX {
     s = h2f(r.sc[C >> 1] >> (16 * (C & 1)));
     c = h2f(r.bi[C >> 1] >> (16 * (C & 1))) - 1024.f * s;
   }
+  // chain C with the weights dequantised to fp16 (s q + b, rounded once); nibbles
+  // 1 and 3 of each half are used in place as 16 q with the scale / 16
+  template <int C>
+  __device__ static void dq(const f16x8* xu, const Raw& r, f32x4& acc) {
+    const float sg = h2f(r.sc[C >> 1] >> (16 * (C & 1)));
+    const float s0 = sg * 16777216.f, s1 = sg * 1048576.f;
+    const float c = h2f(r.bi[C >> 1] >> (16 * (C & 1)));
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const uint32_t w = r.q[C * CH + i], w8 = w >> 8;
+      // (e0,e4) (16e1,16e5) (e2,e6) (16e3,16e7): the xload order
+      const u32x4 b = {xs_dq2(w & 0x000F000Fu, s0, c), xs_dq2(w & 0x00F000F0u, s1, c), xs_dq2(w8 & 0x000F000Fu, s0, c),
+                       xs_dq2(w8 & 0x00F000F0u, s1, c)};
+      acc = xs_mfma32(xu[C * CH + i], b, acc);
+    }
+  }
 };
 
 // Q6_K: unit = one 210-byte super-block (2-byte aligned in the row).  One chain per
@@ -265,7 +315,46 @@ struct XsQ6K {
     s = h2f(r.d) * (float)(int8_t)((r.scw[C >> 2] >> (8 * (C & 3))) & 0xFFu);
     c = -1056.f * s;                              // (q - 32) with q stored as 1024 + q
   }
+  // the 6-bit values of chain C, one per byte (elements 4 kq .. + 3 of group C)
+  template <int C>
+  __device__ static uint32_t q6(const Raw& r) {
+    constexpr int S = C >> 1, g2 = C & 1, h = S >> 2, s = S & 3;
+    const uint32_t ql = r.ql[4 * h + 2 * (s & 1) + g2], qh = r.qh[2 * h + g2];
+    return ((ql >> (4 * (s >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * s)) & 0x03030303u) << 4);
+  }
+  // chains C - 1 and C (odd C: the two halves of slot C / 2) with the weights
+  // dequantised to fp16 (d sc (q - 32), rounded once), one 16x16x32 MFMA
+  template <int C>
+  __device__ static void dq(const f16x8* xu, const Raw& r, f32x4& acc) {
+    if constexpr (C & 1) {
+      const float d = h2f(r.d);
+      const float sa = d * (float)(int8_t)((r.scw[(C - 1) >> 2] >> (8 * ((C - 1) & 3))) & 0xFFu);
+      const float sb = d * (float)(int8_t)((r.scw[C >> 2] >> (8 * (C & 3))) & 0xFFu);
+      const uint32_t va = q6<C - 1>(r), vb = q6<C>(r);
+      const float ma = sa * 16777216.f, mb = sb * 16777216.f, ca = -32.f * sa, cb = -32.f * sb;
+      const u32x4 b = {xs_dq2(__builtin_amdgcn_perm(0u, va, 0x0c010c00u), ma, ca),
+                       xs_dq2(__builtin_amdgcn_perm(0u, va, 0x0c030c02u), ma, ca),
+                       xs_dq2(__builtin_amdgcn_perm(0u, vb, 0x0c010c00u), mb, cb),
+                       xs_dq2(__builtin_amdgcn_perm(0u, vb, 0x0c030c02u), mb, cb)};
+      acc = xs_mfma32(xu[C >> 1], b, acc);
+    }
+  }
 };
+
+// The same providers with the weights dequantised to fp16 before the MFMA (one
+// rounding per weight) and accumulated across chains in the MFMA: no per-chain fp32
+// fold and no activation sums.
+template <class P>
+struct XsDQ : P {
+  static constexpr bool DQ = true;
+  __device__ static void dq_unit(const f16x8* xu, const typename P::Raw& r, f32x4& acc) {
+    xs_static_for<0, P::NCH>([&](auto cc) { P::template dq<decltype(cc)::value>(xu, r, acc); });
+  }
+};
+template <class P, class = void>
+struct XsIsDQ : std::false_type {};
+template <class P>
+struct XsIsDQ<P, std::void_t<decltype(P::DQ)>> : std::bool_constant<P::DQ> {};
 
 // ---------------------------------------------------------------- jobs
 // MODE 0: dense y[t, n] = x[t] . W[n] for t < M (x [M, xld] fp16, y fp16 or fp32).
@@ -314,13 +403,6 @@ __device__ __forceinline__ float xs_act(int act, float v) {
   return 0.5f * v * (1.f + tanhf(u));
 }
 
-template <int I, int N, class Fn>
-__device__ __forceinline__ void xs_static_for(Fn&& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>());
-    xs_static_for<I + 1, N>(f);
-  }
-}
 
 // NS: sub-blocks per wave (8 or 16); TT: token slots folded per lane (lanes 16 kq
 // hold tokens 4 kq .. 4 kq + 3, so at most TT <= 4 active rows need only the first
@@ -463,18 +545,26 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
 #pragma unroll
       for (int u = 0; u < UPW; ++u) {
         if (u >= nu) break;                      // uniform; keeps xa[] statically indexed
+        if constexpr (XsIsDQ<P>::value) {
+#pragma unroll
+          for (int mi = 0; mi < NM; ++mi) P::dq_unit(&xa[8 * u], raw[r][mi][u], acc[mi]);
+          continue;
+        }
         xs_static_for<0, NCH>([&](auto cc) {
           constexpr int C = decltype(cc)::value;
-          const f32x4 xsum = *(const f32x4*)&Xs[((wave * UPW + u) * NCH + C) * 16 + 4 * kq];
+          if constexpr (XsIsDQ<P>::value) {
+          } else {
+            const f32x4 xsum = *(const f32x4*)&Xs[((wave * UPW + u) * NCH + C) * 16 + 4 * kq];
 #pragma unroll
-          for (int mi = 0; mi < NM; ++mi) {
-            const f32x4 d = P::template chain<C>(&xa[8 * u], raw[r][mi][u]);
-            float sc, off;
-            P::template sc<C>(raw[r][mi][u], sc, off);
+            for (int mi = 0; mi < NM; ++mi) {
+              const f32x4 d = P::template chain<C>(&xa[8 * u], raw[r][mi][u]);
+              float sc, off;
+              P::template sc<C>(raw[r][mi][u], sc, off);
 #pragma unroll
-            for (int tt = 0; tt < TTR; ++tt) {
-              const float dv = d[tt];
-              acc[mi][tt] += sc * dv + off * xsum[tt];
+              for (int tt = 0; tt < TTR; ++tt) {
+                const float dv = d[tt];
+                acc[mi][tt] += sc * dv + off * xsum[tt];
+              }
             }
           }
         });
@@ -483,7 +573,9 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
       for (int mi = 0; mi < NM; ++mi)
         *(f32x4*)&red[((wave * RT + r) * 64 + lane) * (4 * NM) + 4 * mi] = acc[mi];
     }
-    __syncthreads();
+    // LDS-only barriers: a __syncthreads would also wait for the next tiles' weights
+    // (its fence drains every outstanding load), serialising the prefetch
+    lds_barrier();
     // fixed-order sum over the waves; thread -> (tile r, lane l, token slot tt)
     for (int e = threadIdx.x; e < RT * 256; e += 64 * W) {
       const int r = e >> 8, l = (e >> 2) & 63, tt = e & 3;
@@ -505,23 +597,32 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
         j.part[(int64_t)(p0 + tk) * j.N + n] = v0 * tsc[tk];
       }
     }
-    __syncthreads();
+    lds_barrier();                                // red[] is reused by the next tiles
   };
 
   Raw ra[RT][NM][UPW];
   int t = blockIdx.x * RT;
-  load_x();                                      // x first: its sums overlap the weight loads
-  load_tiles(ra, t);
-  // X per chain: tokens 4kq .. 4kq+3 in lane 16 kq
-#pragma unroll
-  for (int u = 0; u < UPW; ++u) {
-    xs_static_for<0, NCH>([&](auto cc) {
-      constexpr int C = decltype(cc)::value;
-      const f32x4 X = P::template xsum<C>(&xa[8 * u]);
-      if (n16 == 0) *(f32x4*)&Xs[((wave * UPW + u) * NCH + C) * 16 + 4 * kq] = X;
-    });
+  if constexpr (XsIsDQ<P>::value) {
+    // weights first: the activations' reorder waits for their loads, which then
+    // overlap the weights' instead of preceding them
+    load_tiles(ra, t);
+    load_x();
+  } else {
+    load_x();                                    // x first: its sums overlap the weight loads
+    load_tiles(ra, t);
   }
-  __syncthreads();
+  // X per chain: tokens 4kq .. 4kq+3 in lane 16 kq
+  if constexpr (!XsIsDQ<P>::value) {
+#pragma unroll
+    for (int u = 0; u < UPW; ++u) {
+      xs_static_for<0, NCH>([&](auto cc) {
+        constexpr int C = decltype(cc)::value;
+        const f32x4 X = P::template xsum<C>(&xa[8 * u]);
+        if (n16 == 0) *(f32x4*)&Xs[((wave * UPW + u) * NCH + C) * 16 + 4 * kq] = X;
+      });
+    }
+    __syncthreads();
+  }
   auto run = [&](auto ttc) {
     if constexpr (PIPE) {
       Raw rc[RT][NM][UPW];

@@ -81,7 +81,9 @@ typedef enum {
  *   tiles, 3 wave rows with buffer loads and DPP reductions, 4 rows staged through
  *   LDS by aligned 16-byte loads (Q6_K, Q5_0, Q8_0, Q4_K wire blocks).  MFMA GEMV
  *   (M <= 16): 1 16x16x32 tiles, 5 Q4_K 4x4x4 broadcast tiles, 6 Q4_K x-stationary
- *   tiles, 7 x-stationary tiles of any format that has them.  GEMM: 1 generic
+ *   tiles, 7 x-stationary tiles of any format that has them, 8 x-stationary tiles
+ *   with the weights dequantised to fp16 before the MFMA (Q4_K, Q6_K, MLX), 9 the
+ *   LDS-staged rows of variant 4 for up to 8 rows of x.  GEMM: 1 generic
  *   128x128 tiles, 4 / 5 / 6 / 7 / 8 Q4_K tiles of 256x256 / 128x256 / 128x128 /
  *   64x256 / 64x128 (no K split).
  * No reference counterpart as a single op: the reference dispatches per format

@@ -154,8 +154,9 @@ def test_gemv_mfma(dev, fmt, M):
         check(y, x, wt.W, f"{fmt} gemv_mfma M={M} rg={rg}")
     if fmt in ("q4_k", "q6_k", "mlx_q4") and M <= 16:
         # every kernel explicitly: 1 = 16x16x32 tiles, 5 = 4x4x4 broadcast (Q4_K),
-        # 6 = x-stationary 16x16x32 (Q4_K), 7 = generic x-stationary (Q4_K, Q6_K, MLX)
-        for variant in ((1, 5, 6, 7) if fmt == "q4_k" else (1, 7)):
+        # 6 = x-stationary 16x16x32 (Q4_K), 7 = generic x-stationary (Q4_K, Q6_K, MLX),
+        # 8 = x-stationary with fp16-dequantised weights (Q4_K, Q6_K, MLX)
+        for variant in ((1, 5, 6, 7, 8) if fmt == "q4_k" else (1, 7, 8)):
             y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=variant << 36).cpu().numpy()
             check(y, x, wt.W, f"{fmt} gemv_mfma M={M} variant={variant}")
 
@@ -229,6 +230,15 @@ def _sampled(fmt, N, K, M, dev, seed, path="auto"):
     check(y[:, rows], xs, W, f"{fmt} {M}x{K}x{N} {path}")
 
 
+@pytest.mark.parametrize("fmt,M,K,N", [("q4_k", 9, 2048, 13000), ("q6_k", 5, 1024, 12301), ("q4_k", 16, 8192, 200),
+                                        ("q4_k", 13, 1024, 5000)])
+def test_gemv_dequant_xs_launches(dev, fmt, M, K, N):
+    # the default M <= 16 kernel for Q4_K / Q6_K with fp16-dequantised weights: one
+    # workgroup per CU looping over the tiles (N >= 12288, partial last tile), 16-slot
+    # waves (K = 8192), two tiles per reduction (Q4_K, M > 8, mid-size N)
+    _sampled(fmt, N, K, M, dev, seed=M + K + N)
+
+
 LLAMA32_3B = [(3072, 3072), (3072, 1024), (3072, 8192), (8192, 3072), (3072, 128256)]   # (K, N)
 LLAMA3_8B = [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)]
 
@@ -264,7 +274,7 @@ def test_gemv_xs_mlx_group_sizes(dev, gs):
     wt = Weight("mlx_q4", N, K, rng, dev, gs=gs)
     x = synth.numpy_x(M, K, rng)
     xt = torch.from_numpy(x).to(dev)
-    for variant in (0, 7):
+    for variant in (0, 7, 8):
         y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=variant << 36).cpu().numpy()
         check(y, x, wt.W, f"mlx_q4 gs={gs} gemv_mfma M={M} variant={variant}")
 
