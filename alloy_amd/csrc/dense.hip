@@ -1413,10 +1413,10 @@ static hipError_t launch_gemv_xs(int fmt, const QArgs& a, const void* x, bool x_
   j.sb = (uint32_t)(a.K / a.gs * 2);
   if (dq) {
     switch (a.gs) {
-      case 32: return launch_xs<XsDQ<XsMLX<0>>, 0>(j, 0, cap, o.row_groups, st);
-      case 64: return launch_xs<XsDQ<XsMLX<1>>, 0>(j, 0, cap, o.row_groups, st);
-      case 128: return launch_xs<XsDQ<XsMLX<2>>, 0>(j, 0, cap, o.row_groups, st);
-      default: return a.gs == 256 ? launch_xs<XsDQ<XsMLX<3>>, 0>(j, 0, cap, o.row_groups, st) : hipErrorNotSupported;
+      case 32: return launch_xs<XsMLXD<0>, 0>(j, 0, cap, o.row_groups, st);
+      case 64: return launch_xs<XsMLXD<1>, 0>(j, 0, cap, o.row_groups, st);
+      case 128: return launch_xs<XsMLXD<2>, 0>(j, 0, cap, o.row_groups, st);
+      default: return a.gs == 256 ? launch_xs<XsMLXD<3>, 0>(j, 0, cap, o.row_groups, st) : hipErrorNotSupported;
     }
   }
   switch (a.gs) {
@@ -1479,7 +1479,8 @@ hipError_t launch_glu_combine(int act, const float* g, const float* u, void* y, 
 //         x-stationary kernel with fp16-dequantised weights (8); else the Q4_K
 //         x-stationary kernel
 //   Q6_K  K <= 4096: x-stationary with fp16-dequantised weights, else 16x16x32
-//   MLX   generic x-stationary (exact products; dequantising measured no faster)
+//   MLX   generic x-stationary (exact products); N >= 12288: the dequantising
+//         provider with 16-byte loads, one workgroup per CU looping over the tiles
 //   other formats (and shapes the above do not take): 16x16x32 kernel
 static int mfma_variant(int fmt, int64_t M, int64_t N, int64_t K) {
   if (fmt == F_Q4_K) {
@@ -1487,7 +1488,7 @@ static int mfma_variant(int fmt, int64_t M, int64_t N, int64_t K) {
     return K <= 8192 ? 8 : 6;
   }
   if (fmt == F_Q6_K) return K <= 4096 ? 8 : 1;
-  if (fmt == F_MLX) return 7;
+  if (fmt == F_MLX) return N >= 12288 ? 8 : 7;
   return 1;
 }
 

@@ -229,22 +229,6 @@ struct XsMLX {
     s = h2f(r.sc[C >> 1] >> (16 * (C & 1)));
     c = h2f(r.bi[C >> 1] >> (16 * (C & 1))) - 1024.f * s;
   }
-  // chain C with the weights dequantised to fp16 (s q + b, rounded once); nibbles
-  // 1 and 3 of each half are used in place as 16 q with the scale / 16
-  template <int C>
-  __device__ static void dq(const f16x8* xu, const Raw& r, f32x4& acc) {
-    const float sg = h2f(r.sc[C >> 1] >> (16 * (C & 1)));
-    const float s0 = sg * 16777216.f, s1 = sg * 1048576.f;
-    const float c = h2f(r.bi[C >> 1] >> (16 * (C & 1)));
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      const uint32_t w = r.q[C * CH + i], w8 = w >> 8;
-      // (e0,e4) (16e1,16e5) (e2,e6) (16e3,16e7): the xload order
-      const u32x4 b = {xs_dq2(w & 0x000F000Fu, s0, c), xs_dq2(w & 0x00F000F0u, s1, c), xs_dq2(w8 & 0x000F000Fu, s0, c),
-                       xs_dq2(w8 & 0x00F000F0u, s1, c)};
-      acc = xs_mfma32(xu[C * CH + i], b, acc);
-    }
-  }
 };
 
 // Q6_K: unit = one 210-byte super-block (2-byte aligned in the row).  One chain per
@@ -337,6 +321,91 @@ struct XsQ6K {
                        xs_dq2(__builtin_amdgcn_perm(0u, vb, 0x0c010c00u), mb, cb),
                        xs_dq2(__builtin_amdgcn_perm(0u, vb, 0x0c030c02u), mb, cb)};
       acc = xs_mfma32(xu[C >> 1], b, acc);
+    }
+  }
+};
+
+// MLX 4-bit affine with the weights dequantised to fp16 (s q + b, rounded once), any
+// group size 32 << GSH: every lane reads two 16-byte runs of four words (words 4 kq
+// .. + 3 and 16 + 4 kq .. + 3 of the unit; MFMA S takes word 16 (S / 4) + 4 kq + S % 4),
+// whatever the group size, since one MFMA may now span scale groups; each lane
+// decodes the scale / bias of its two groups only.  Half the load instructions of the
+// exact-integer MLX provider at group size 32 / 64.
+template <int GSH>
+struct XsMLXD {
+  static constexpr int G = GSH >= 3 ? 1 : 8 >> GSH;     // groups per unit
+  static constexpr int NW = G >= 2 ? G / 2 : 1;         // scale words per unit
+  static constexpr int NCH = 8;
+  static constexpr bool WIDE = true;
+  static constexpr bool DQ = true;
+  struct Raw { u32x4 q0, q1; uint32_t sc[NW], bi[NW]; };
+  __device__ static void load(const Src& src, uint32_t rw, uint32_t rs, int unit, int kq, Raw& r) {
+    const uint32_t bo = rw + (uint32_t)unit * 128u + 16u * kq;
+    r.q0 = bld16(src.w, bo);
+    r.q1 = bld16(src.w, bo + 64u);
+    if constexpr (G == 8) {
+      const uint32_t so = rs + 16u * unit;
+      const u32x4 s4 = bld16(src.s, so), b4 = bld16(src.b, so);
+      r.sc[0] = s4.x; r.sc[1] = s4.y; r.sc[2] = s4.z; r.sc[3] = s4.w;
+      r.bi[0] = b4.x; r.bi[1] = b4.y; r.bi[2] = b4.z; r.bi[3] = b4.w;
+    } else if constexpr (G == 4) {
+      const uint32_t so = rs + 8u * unit;
+      const uint2 s2 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(src.s, so, 0, 0));
+      const uint2 b2 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(src.b, so, 0, 0));
+      r.sc[0] = s2.x; r.sc[1] = s2.y;
+      r.bi[0] = b2.x; r.bi[1] = b2.y;
+    } else if constexpr (G == 2) {
+      r.sc[0] = bld4(src.s, rs + 4u * unit);
+      r.bi[0] = bld4(src.b, rs + 4u * unit);
+    } else {
+      const uint32_t so = rs + 2u * (((uint32_t)unit << 3) >> GSH);
+      r.sc[0] = bld2(src.s, so);
+      r.bi[0] = bld2(src.b, so);
+    }
+  }
+  __device__ static uint32_t word(int S, int kq) { return (uint32_t)(16 * (S >> 2) + 4 * kq + (S & 3)); }
+  __device__ static f16x8 xload(__amdgpu_buffer_rsrc_t xr, uint32_t off, int S, int kq) {
+    return xs_x8_perm8(xr, off + 16u * word(S, kq));
+  }
+  __device__ static void xload32(__amdgpu_buffer_rsrc_t xr, uint32_t off, int S, int kq, float (&v)[8]) {
+    xs_x8_f32<0, 4, 1, 5, 2, 6, 3, 7>(xr, off + 32u * word(S, kq), v);
+  }
+  // scale and bias halves (as dwords shifted into the low half) of the lane's group for
+  // words 16 h + 4 kq + (0..3): group (16 h + 4 kq) >> (2 + GSH)
+  __device__ static void group(const Raw& r, int h, int kq, uint32_t& sc, uint32_t& bi) {
+    if constexpr (GSH == 0) {                      // group 4 h + kq: word 2 h + kq / 2, half kq % 2
+      const int wd = kq >> 1, sh = 16 * (kq & 1);
+      sc = (wd ? r.sc[2 * h + 1] : r.sc[2 * h]) >> sh;
+      bi = (wd ? r.bi[2 * h + 1] : r.bi[2 * h]) >> sh;
+    } else if constexpr (GSH == 1) {               // group 2 h + kq / 2: word h, half kq / 2
+      const int sh = 16 * (kq >> 1);
+      sc = r.sc[h] >> sh;
+      bi = r.bi[h] >> sh;
+    } else if constexpr (GSH == 2) {               // group h
+      sc = r.sc[0] >> (16 * h);
+      bi = r.bi[0] >> (16 * h);
+    } else {
+      sc = r.sc[0];
+      bi = r.bi[0];
+    }
+  }
+  __device__ static void dq_unit(const f16x8* xu, const Raw& r, f32x4& acc) {
+    const int kq = (int)(threadIdx.x >> 4) & 3;
+    const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t scw, biw;
+      group(r, h, kq, scw, biw);
+      const float sg = h2f(scw), c = h2f(biw);
+      const float s0 = sg * 16777216.f, s1 = sg * 1048576.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t w = q[4 * h + i], w8 = w >> 8;
+        // (e0,e4) (16e1,16e5) (e2,e6) (16e3,16e7): the xload order
+        const u32x4 b = {xs_dq2(w & 0x000F000Fu, s0, c), xs_dq2(w & 0x00F000F0u, s1, c), xs_dq2(w8 & 0x000F000Fu, s0, c),
+                         xs_dq2(w8 & 0x00F000F0u, s1, c)};
+        acc = xs_mfma32(xu[4 * h + i], b, acc);
+      }
     }
   }
 };
