@@ -6,7 +6,8 @@ down) + lm_head = 197 GEMVs over 1,807,073,280 weight bytes (synthetic weights w
 the benchmark distribution, fp16 N(0,1) activations, fp32 output).  The weight set
 is 7x the 256 MB Infinity Cache, so every launch streams its weights from HBM.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--suite PATH]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill] [--no-configs]
+                    [--decode-only [--eager]] [--configs-only] [--copy-calibration]
 
 Prints ONE JSON line.  The step's 197 launches are captured once in a HIP graph (the decode loop is
 launch-bound otherwise); ``value`` = total weight bytes x K / elapsed time of K
@@ -214,20 +215,33 @@ def prefill_gemm(dev, qmm, Ms=(512, 2048, 4096), reps=10):
     return out
 
 
-def _rotating_time(dev, fn_for, copies, reps=5):
+def _rotating_time(dev, fn_for, copies, reps=5, eager=False):
     """Average seconds per call of fn_for(copy) over a graph that cycles through
-    `copies` (together larger than the 256 MB Infinity Cache, so weights come from HBM)."""
+    `copies` (together larger than the 256 MB Infinity Cache, so weights come from HBM);
+    eager: the same calls launched directly (counter runs)."""
     import torch
 
     seq = copies * max(1, 24 // len(copies))
     stream = torch.cuda.current_stream(dev)
+    if eager:
+        for c in seq:
+            fn_for(c)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(reps):
+            for c in seq:
+                fn_for(c)
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / 1000.0 / (reps * len(seq))
     g = capture(lambda: [fn_for(c) for c in seq], dev)
     t = time_replays(g, reps, 2, stream) / (reps * len(seq))
     del g
     return t
 
 
-def other_configs(dev, qmm):
+def other_configs(dev, qmm, eager=False):
     """The other BASELINE configurations, on the GPU: config 1 (Q8_0 4096x4096, M=1,
     fp32 out), config 3 (Q6_K and Q5_0 at Llama-3-8B shapes, M=1 and M=8) and config 5
     (MLX 4-bit MoE, 128 experts, top-8, H=2048, I=768, T in {1, 16, 256}); config 2 is
@@ -244,7 +258,7 @@ def other_configs(dev, qmm):
         ws = [synth.torch_blocks(fmt, N, K, seed + i, dev) for i in range(ncopy)]
         x = synth.torch_x(M, K, seed, dev)
         y = torch.empty((M, N), dtype=torch.float32, device=dev)
-        t = _rotating_time(dev, lambda w: qmm(fmt, x, w, out=y), ws)
+        t = _rotating_time(dev, lambda w: qmm(fmt, x, w, out=y), ws, eager=eager)
         del ws
         return {"us": round(t * 1e6, 2), "GBps": round(nbytes / t / 1e9, 1),
                 "frac_hbm_peak": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
@@ -275,7 +289,7 @@ def other_configs(dev, qmm):
     for T in (1, 16, 256):
         x = synth.torch_x(T, H, 600 + T, dev)
         lg = torch.randn((T, E), device=dev, generator=torch.Generator(device=dev).manual_seed(T))
-        t = _rotating_time(dev, lambda c: torch.ops.alloy.mlx_moe_routed(x, lg, *c, E, k, I), experts)
+        t = _rotating_time(dev, lambda c: torch.ops.alloy.mlx_moe_routed(x, lg, *c, E, k, I), experts, eager=eager)
         touched = int(torch.unique(torch.topk(lg, k, dim=1).indices).numel())
         moe[f"T{T}"] = {"us": round(t * 1e6, 1), "experts_touched": touched,
                         "GBps_touched_weights": round(touched * per_expert / t / 1e9, 1)}
@@ -323,9 +337,11 @@ def main():
     ap.add_argument("--decode-only", action="store_true",
                     help="time the decode step only (no per-shape, prefill or CPU legs)")
     ap.add_argument("--eager", action="store_true",
-                    help="launch the decode step eagerly instead of replaying a HIP graph (counter runs)")
+                    help="launch eagerly instead of replaying HIP graphs (counter runs; decode step or configs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 256 MiB device copy (counter calibration) and exit")
+    ap.add_argument("--configs-only", action="store_true",
+                    help="time only the other BASELINE configurations (profiler runs of their kernels)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -342,6 +358,9 @@ def main():
         copy_calibration(dev)
         return
     alloy_amd.lib()
+    if args.configs_only:
+        print(json.dumps({"other_configs": other_configs(dev, qmm, eager=args.eager), "eager": args.eager}))
+        return
     log("building decode step weights ...")
     mats, xs, ys = build_decode_step(dev)
     total_bytes = sum(q4k_bytes(K, N) for _, K, N, _ in mats)
