@@ -1500,7 +1500,7 @@ hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, 
   // measured on the BASELINE decode shapes at M = 2, 4, 8
   const bool unaligned = fmt == F_Q6_K || fmt == F_Q5_0 || fmt == F_Q8_0;
   const bool tile_small_m = unaligned ? (M == 2 || M * N <= 8192)
-                                      : fmt == F_Q4_K && ((M == 2 && (N <= 1024 || a.K >= 8192)) || (M <= 4 && N <= 1024));
+                                      : fmt == F_Q4_K && M == 2 && (N <= 1024 || a.K >= 8192);
   const int v = o.variant ? o.variant : tile_small_m ? 9 : mfma_variant(fmt, M, N, a.K);
   hipError_t e = hipErrorNotSupported;
   if (v == 9) e = launch_gemv_tile(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
