@@ -132,6 +132,7 @@ alloy_status alloy_qmm_ws(alloy_format fmt, const void* w, const void* aux, cons
   o.row_groups = (int)((opts >> 28) & 0xF);
   o.depth = (int)((opts >> 32) & 0xF);
   o.variant = (int)((opts >> 36) & 0xF);
+  o.splits = (int)((opts >> 40) & 0xF);
   if (o.lanes_per_row && (o.lanes_per_row % 16 || o.lanes_per_row > 256))
     return fail(ALLOY_E_ARG, "lanes_per_row %d must be a multiple of 16 in [16, 256]", o.lanes_per_row);
   int p = (int)path;

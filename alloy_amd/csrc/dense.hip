@@ -1534,20 +1534,25 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float* ws, int S, int6
 }
 
 // Q4_K GEMM plan: tile kind (0 = 256x256, 1 = 128x256, 2 = 128x128, 3 = 64x256,
-// 4 = 64x128) and K splits S.  Each kind's measured full-chip rate (TFLOP/s on
-// MI355X) is scaled by the fraction of CU slots its tile count x S fills in the last
-// round of workgroups; a split adds the partial-sum pass ((S+1) fp32 M x N tiles of
-// HBM traffic) and one launch.  S divides the super-blocks, at least two per split.
+// 4 = 64x128; 5 = 256x256 and 6 = 256x128 with one wave per SIMD, gemm_q4k.hip) and
+// K splits S.  Each kind's measured full-chip rate (TFLOP/s on MI355X) is scaled by
+// the fraction of CU slots its tile count x S fills in the last round of workgroups; a
+// split adds the partial-sum pass ((S+1) fp32 M x N tiles of HBM traffic) and one
+// launch.  S divides the super-blocks, at least two per split.  Kinds 5 and 6 are
+// not planned (rate 0; forced variants 9 / 10 only): measured in the same run, kind 5
+// is 3-5 % below kind 0 on the same tile and kind 6 5-8 % below kind 1 at every shape
+// and split count of the prefill configurations.
 struct GemmPlan { int kind, splits; };
 static GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K, bool allow_split) {
   const int cus = xs_cu_count();
-  const int bm[5] = {256, 128, 128, 64, 64}, bn[5] = {256, 256, 128, 256, 128};
-  const double rate[5] = {1000e12, 790e12, 600e12, 590e12, 420e12};
+  const int bm[7] = {256, 128, 128, 64, 64, 256, 256}, bn[7] = {256, 256, 128, 256, 128, 256, 128};
+  const double rate[7] = {1000e12, 790e12, 600e12, 590e12, 420e12, 0, 0};
   const double flops = 2.0 * (double)M * (double)N * (double)K;
   const int64_t sb = K / 256;
   GemmPlan best{0, 1};
   double best_t = 1e30;
-  for (int k = 0; k < 5; ++k) {
+  for (int k = 0; k < 7; ++k) {
+    if (rate[k] <= 0) continue;
     const int64_t tl = ((M + bm[k] - 1) / bm[k]) * ((N + bn[k] - 1) / bn[k]);
     for (int S = 1; S <= (allow_split ? 4 : 1); ++S) {
       if (S > 1 && (sb % S || sb / S < 2)) continue;
@@ -1578,10 +1583,28 @@ struct GemmRun {
     if constexpr (std::is_same<F, FQ4K>::value) {
       if (!x_f32 && gemm_q4k_fits(M, N, a) && (M > 64 || o.variant >= 4) && o.variant != 1) {
         GemmPlan p = o.variant >= 4 ? GemmPlan{o.variant - 4, 1} : gemm_plan(M, N, a.K, ws != nullptr);
+        if (o.variant >= 4 && o.splits > 1 && (a.K / 256) % o.splits == 0 && a.K / 256 / o.splits >= 2)
+          p.splits = o.splits;             // forced split (falls back to none without the workspace)
         if (p.splits > 1 &&
             (ws_bytes < (int64_t)p.splits * M * N * 4 || ((uintptr_t)ws & 15) || ((uintptr_t)y & 15) || (M * N) % 4))
-          p = gemm_plan(M, N, a.K, false);
+          p = o.variant >= 4 ? GemmPlan{p.kind, 1} : gemm_plan(M, N, a.K, false);
         const int nsb = p.splits > 1 ? (int)(a.K / 256 / p.splits) : 0;
+        auto sum_splits = [&]() {
+          const int64_t mn = M * N, blocks = (mn / 4 + 255) / 256;
+          if (y_f32)
+            hipLaunchKernelGGL(k_splitk_sum<float>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)ws,
+                               p.splits, mn, (float*)y);
+          else
+            hipLaunchKernelGGL(k_splitk_sum<f16>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)ws,
+                               p.splits, mn, (f16*)y);
+          return hipGetLastError();
+        };
+        if (p.kind >= 5) {                 // one wave per SIMD (gemm_q4k.hip)
+          const bool split = p.splits > 1;
+          hipError_t e = launch_gemm_q4k_w4(p.kind - 5, a, (const f16*)x, (int)M, split ? ws : y, split || y_f32,
+                                            (int)N, p.splits, nsb, st);
+          return e != hipSuccess || !split ? e : sum_splits();
+        }
         auto go = [&](auto mi, auto ni) {
           constexpr int MI = decltype(mi)::value, NI = decltype(ni)::value;
           const dim3 grid((unsigned)((N + 128 * NI - 1) / (128 * NI)), (unsigned)((M + 64 * MI - 1) / (64 * MI)),
@@ -1596,15 +1619,7 @@ struct GemmRun {
             hipLaunchKernelGGL((k_gemm_q4k<MI, NI, f16>), grid, dim3(512), 0, st, a, (const f16*)x, (int)M,
                                (f16*)y, (int)N, 0);
           hipError_t e = hipGetLastError();
-          if (e != hipSuccess || p.splits == 1) return e;
-          const int64_t mn = M * N, blocks = (mn / 4 + 255) / 256;
-          if (y_f32)
-            hipLaunchKernelGGL(k_splitk_sum<float>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)ws,
-                               p.splits, mn, (float*)y);
-          else
-            hipLaunchKernelGGL(k_splitk_sum<f16>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)ws,
-                               p.splits, mn, (f16*)y);
-          return hipGetLastError();
+          return e != hipSuccess || p.splits == 1 ? e : sum_splits();
         };
         switch (p.kind) {
           case 0: return go(std::integral_constant<int, 4>(), std::integral_constant<int, 2>());

@@ -8,6 +8,7 @@ is 7x the 256 MB Infinity Cache, so every launch streams its weights from HBM.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill] [--no-configs]
                     [--decode-only [--eager]] [--configs-only] [--copy-calibration]
+    python bench.py --prefill-only [--eager] [--gemm-opts N]
 
 Prints ONE JSON line.  The step's 197 launches are captured once in a HIP graph (the decode loop is
 launch-bound otherwise); ``value`` = total weight bytes x K / elapsed time of K
@@ -195,7 +196,9 @@ def cpu_baseline(seconds_target=15.0):
     }
 
 
-def prefill_gemm(dev, qmm, Ms=(512, 2048, 4096), reps=10):
+def prefill_gemm(dev, qmm, Ms=(512, 2048, 4096), reps=10, opts=0, eager=False):
+    """Q4_K GEMM on the config-4 shapes; opts: forced tile / split (bits 36-39, 40-43);
+    eager: direct launches timed by events (counter runs) instead of graph replays."""
     import torch
 
     from alloy_amd import synth
@@ -206,8 +209,20 @@ def prefill_gemm(dev, qmm, Ms=(512, 2048, 4096), reps=10):
         x = synth.torch_x(M, K, 78 + K, dev)
         y = torch.empty((M, N), dtype=torch.float32, device=dev)
         stream = torch.cuda.current_stream(dev)
-        g = capture(lambda: qmm("q4_k", x, w, out=y, path="gemm"), dev)
-        t = time_replays(g, reps, 2, stream) / reps
+        fn = lambda: qmm("q4_k", x, w, out=y, path="gemm", opts=opts)  # noqa: E731
+        if eager:
+            fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            t = e0.elapsed_time(e1) / 1000.0 / reps
+        else:
+            g = capture(fn, dev)
+            t = time_replays(g, reps, 2, stream) / reps
         tf = 2.0 * M * N * K / t / 1e12
         out.append({"M": M, "K": K, "N": N, "us": round(t * 1e6, 1), "tflops": round(tf, 2),
                     "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)})
@@ -342,6 +357,10 @@ def main():
                     help="run only a 256 MiB device copy (counter calibration) and exit")
     ap.add_argument("--configs-only", action="store_true",
                     help="time only the other BASELINE configurations (profiler runs of their kernels)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="time only the config-4 prefill GEMMs (with --eager: direct launches)")
+    ap.add_argument("--gemm-opts", type=int, default=0,
+                    help="alloy_qmm opts for --prefill-only: forced Q4_K tile (bits 36-39) and K splits (40-43)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -360,6 +379,10 @@ def main():
     alloy_amd.lib()
     if args.configs_only:
         print(json.dumps({"other_configs": other_configs(dev, qmm, eager=args.eager), "eager": args.eager}))
+        return
+    if args.prefill_only:
+        print(json.dumps({"prefill_gemm": prefill_gemm(dev, qmm, opts=args.gemm_opts, eager=args.eager),
+                          "gemm_opts": args.gemm_opts, "eager": args.eager}))
         return
     log("building decode step weights ...")
     mats, xs, ys = build_decode_step(dev)

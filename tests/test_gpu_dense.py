@@ -171,8 +171,9 @@ def test_gemm(dev, fmt, M, N, K):
     y = wt.qmm(xt, path="gemm", out_dtype=torch.float32).cpu().numpy()
     check(y, x, wt.W, f"{fmt} gemm M={M} N={N} K={K}")
     if fmt == "q4_k":
-        # every kernel: 1 = 128x128 generic, 4/5/6 = Q4_K 256x256 / 128x256 / 128x128 tiles
-        for variant in (1, 4, 5, 6):
+        # every kernel: 1 = 128x128 generic, 4/5/6 = Q4_K 256x256 / 128x256 / 128x128 tiles,
+        # 9/10 = Q4_K 256x256 / 256x128 tiles with one wave per SIMD
+        for variant in (1, 4, 5, 6, 9, 10):
             yv = wt.qmm(xt, path="gemm", out_dtype=torch.float32, opts=variant << 36).cpu().numpy()
             check(yv, x, wt.W, f"{fmt} gemm M={M} N={N} K={K} variant={variant}")
 
@@ -181,7 +182,7 @@ def test_gemm(dev, fmt, M, N, K):
 def test_gemm_split_k(dev, M, K, N):
     """Few output tiles: the Q4_K GEMM plan splits K into a workspace and sums the
     slices in order; checked against the oracle for fp32 and fp16 outputs, against the
-    unsplit launch, and for determinism."""
+    unsplit launch, and for determinism; then every Q4_K tile with forced splits."""
     rng = np.random.default_rng(M + N)
     wt = Weight("q4_k", N, K, rng, dev)
     x = synth.numpy_x(M, K, rng)
@@ -199,6 +200,11 @@ def test_gemm_split_k(dev, M, K, N):
                               y1.data_ptr(), 0, M, N, K, 3, 0, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     check(y1.cpu().numpy(), x, wt.W, "unsplit GEMM (no workspace)")
+    # every Q4_K tile with a forced split of 2 and 4
+    for variant in (4, 5, 6, 7, 8, 9, 10):
+        for S in (2, 4):
+            yv = wt.qmm(xt, out_dtype=torch.float32, path="gemm", opts=(variant << 36) | (S << 40))
+            check(yv.cpu().numpy(), x, wt.W, f"GEMM variant={variant} splits={S}")
 
 
 def test_outputs_deterministic_and_f16(dev):
