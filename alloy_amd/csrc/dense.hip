@@ -1540,7 +1540,7 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float* ws, int S, int6
 // split adds the partial-sum pass ((S+1) fp32 M x N tiles of HBM traffic) and one
 // launch.  S divides the super-blocks, at least two per split.  Kinds 5 and 6 are
 // not planned (rate 0; forced variants 9 / 10 only): measured in the same run, kind 5
-// is 3-5 % below kind 0 on the same tile and kind 6 5-8 % below kind 1 at every shape
+// is 2-12 % below kind 0 on the same tile and kind 6 3-8 % below kind 1 at every shape
 // and split count of the prefill configurations.
 struct GemmPlan { int kind, splits; };
 static GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K, bool allow_split) {
