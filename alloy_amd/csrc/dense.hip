@@ -572,32 +572,42 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, 
   const uint32_t wrow = (uint32_t)(n0 + br) * rb + 144u * kb;
 
   struct Blk { u32x4 hd, q[4]; };          // this thread's bytes of one super-block
+  // the super-block / step offsets are uniform: scalar operands of the loads
   auto bload = [&](int sb, Blk& r) {       // past the end: in-bounds garbage or zeros
-    const uint32_t blk = wrow + (uint32_t)sb * 144u;
-    r.hd = bld16(wr, blk);
+    const uint32_t so = (uint32_t)sb * 144u;
+    r.hd = __builtin_amdgcn_raw_buffer_load_b128(wr, wrow, so, 0);
 #pragma unroll
-    for (int p = 0; p < 4; ++p) r.q[p] = bld16(wr, blk + 16u + 32u * p + 16u * (uint32_t)bh);
+    for (int p = 0; p < 4; ++p)
+      r.q[p] = __builtin_amdgcn_raw_buffer_load_b128(wr, wrow + 16u + 32u * p + 16u * (uint32_t)bh, so, 0);
   };
   u32x4 xs[AC];                            // x chunks of the next step
   auto xload = [&](int kt) {
+    const uint32_t so = 2u * (uint32_t)kt * QBK;
 #pragma unroll
-    for (int i = 0; i < AC; ++i) xs[i] = bld16(xr, xoff[i] + 2u * (uint32_t)kt * QBK);
+    for (int i = 0; i < AC; ++i) xs[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[i], so, 0);
   };
   auto astore = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < AC; ++i) *(u32x4*)&As[buf][arow[i]][acol[i]] = xs[i];
   };
   // scales/offsets of sub-blocks 2p (low nibbles) and 2p+1 (high) of pair p; the
-  // nibble halves enter v_fma_mix as fp16 denormals q*2^-24 (16q*2^-24 high)
+  // nibble halves enter v_fma_mix as fp16 denormals q*2^-24 (16q*2^-24 high).  The two
+  // threads of a row (lanes 2i, 2i+1) each decode sub-block 2p+bh and swap the result
+  // with a DPP quad permutation [1,0,3,2].
+  const float smul = bh ? 1048576.f : 16777216.f;      // 2^24 / 16 (high), 2^24 (low)
+  auto swap_pair = [](float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  };
   auto scales = [&](const Blk& r, int p, float (&s)[2], float (&c)[2]) {
-    uint32_t sc0, mn0, sc1, mn1;
-    q4k_scale_min(r.hd.y, r.hd.z, r.hd.w, 2 * p, sc0, mn0);     // p is a constant
-    q4k_scale_min(r.hd.y, r.hd.z, r.hd.w, 2 * p + 1, sc1, mn1);
+    uint32_t sc, mn;
+    q4k_scale_min(r.hd.y, r.hd.z, r.hd.w, 2 * p + bh, sc, mn);   // 2p+bh < 4 iff p < 2
     const float d = h2f(r.hd.x), dmin = h2f(r.hd.x >> 16);
-    s[0] = d * (float)sc0 * 16777216.f;                 // 2^24
-    s[1] = d * (float)sc1 * 1048576.f;                  // 2^24 / 16
-    c[0] = -(dmin * (float)mn0);
-    c[1] = -(dmin * (float)mn1);
+    const float so = d * (float)sc * smul, co = -(dmin * (float)mn);
+    const float sp = swap_pair(so), cp = swap_pair(co);
+    s[0] = bh ? sp : so;
+    s[1] = bh ? so : sp;
+    c[0] = bh ? cp : co;
+    c[1] = bh ? co : cp;
   };
   // quarter j of a step's dequant: word j of the pair -> 4 elements of each sub-block
   auto deq = [&](const u32x4& q, int j, const float (&s)[2], const float (&c)[2], int buf) {
