@@ -1,5 +1,6 @@
-// Dense quantized matmul kernels for gfx950: dequant probe, M=1 GEMV (v_dot2),
-// M<=16 GEMV on MFMA, and the prefill GEMM on MFMA.  All launched on the caller's
+// Dense quantized matmul kernels for gfx950: dequant probe, quantized embedding,
+// M=1 GEMV (v_dot2), M<=16 GEMV on MFMA and the gated pair (the prefill GEMM is in
+// gemm.hip).  All launched on the caller's
 // HIP stream; no allocation, no global mutable state.
 #include <type_traits>
 
@@ -8,22 +9,6 @@
 #include "xs.h"
 
 namespace alloy {
-
-// ------------------------------------------------------------------ helpers
-__device__ __forceinline__ void store_y(void* y, bool y_f32, int64_t i, float v) {
-  if (y_f32) ((float*)y)[i] = v;
-  else ((f16*)y)[i] = (f16)v;
-}
-
-template <class F>
-__device__ __forceinline__ void dec32_f16(const QArgs& a, int64_t n, int k0, f16x8 (&o)[4]) {
-  float w[32];
-  F::dec32(a, n, k0, w);
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[j][e] = (f16)w[8 * j + e];   // RNE
-}
 
 // ------------------------------------------------------------------ dequant probe
 // One thread per (row, 32-element group).  out is [nrows, K] f32 (exact) or f16 (RN).
@@ -434,306 +419,6 @@ __global__ __launch_bounds__(256) void k_gemv_mfma(QArgs a, const XT* x, int M, 
   }
 }
 
-// ------------------------------------------------------------------ prefill GEMM on MFMA
-// Tile 128 (x rows) x 128 (weight rows) x 64 (K), 4 waves as 2x2, each 64x64 from
-// 2x2 v_mfma_f32_32x32x16_f16.  The weight tile is dequantised (exact fp32 -> RN fp16)
-// straight into LDS; x is copied as fp16.
-constexpr int GBM = 128, GBN = 128, GBK = 64, GLD = GBK + 8;
-
-template <class F, typename XT>
-__global__ __launch_bounds__(256) void k_gemm(QArgs a, const XT* x, int M, void* y, int y_f32,
-                                              int64_t N) {
-  __shared__ f16 As[GBM][GLD];
-  __shared__ f16 Bs[GBN][GLD];
-  const int K = a.K;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int64_t m0 = (int64_t)blockIdx.y * GBM;
-  const int64_t n0 = (int64_t)blockIdx.x * GBN;
-  f32x16 acc[2][2];
-#pragma unroll
-  for (int tm = 0; tm < 2; ++tm)
-#pragma unroll
-    for (int tn = 0; tn < 2; ++tn)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[tm][tn][e] = 0.f;
-
-  for (int k0 = 0; k0 < K; k0 += GBK) {
-    // x tile: 128 rows x 8 chunks of 8 halves
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int idx = tid + 256 * c, row = idx >> 3, col = (idx & 7) * 8;
-      const int64_t gm = m0 + row;
-      const int gk = k0 + col;
-      f16x8 v = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      if (gm < M && gk < K) v = ld_x8<XT>(x + gm * K + gk);
-      *(f16x8*)&As[row][col] = v;
-    }
-    // weight tile: 128 rows x 2 groups of 32
-    {
-      const int row = tid >> 1, kh = (tid & 1) * 32;
-      const int64_t gn = n0 + row;
-      f16x8 o[4];
-      if (gn < N && k0 + kh < K) dec32_f16<F>(a, gn, k0 + kh, o);
-      else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) o[j] = f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) *(f16x8*)&Bs[row][kh + 8 * j] = o[j];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int ks = 0; ks < GBK; ks += 16) {
-      f16x8 af[2], bf[2];
-      const int kc = ks + 8 * (lane >> 5);
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        af[t] = *(const f16x8*)&As[64 * wm + 32 * t + (lane & 31)][kc];
-        bf[t] = *(const f16x8*)&Bs[64 * wn + 32 * t + (lane & 31)][kc];
-      }
-#pragma unroll
-      for (int tm = 0; tm < 2; ++tm)
-#pragma unroll
-        for (int tn = 0; tn < 2; ++tn)
-          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[tm], bf[tn], acc[tm][tn], 0, 0, 0);
-    }
-    __syncthreads();
-  }
-  // D[i][j]: j = lane%32 (weight row), i = 8(t/4) + 4(lane/32) + t%4 (x row)
-#pragma unroll
-  for (int tm = 0; tm < 2; ++tm)
-#pragma unroll
-    for (int tn = 0; tn < 2; ++tn) {
-      const int64_t gn = n0 + 64 * wn + 32 * tn + (lane & 31);
-#pragma unroll
-      for (int t = 0; t < 16; ++t) {
-        const int64_t gm = m0 + 64 * wm + 32 * tm + 8 * (t >> 2) + 4 * (lane >> 5) + (t & 3);
-        if (gm < M && gn < N) store_y(y, y_f32, gm * N + gn, acc[tm][tn][t]);
-      }
-    }
-}
-
-// ------------------------------------------------------------------ host launchers
-// ------------------------------------------------------------------ prefill GEMM, Q4_K, 256x256
-// 512 threads = 8 waves as 2 (x rows) x 4 (weight rows); each wave owns a 128x64 output
-// block = 4 x 2 tiles of v_mfma_f32_32x32x16_f16 (128 fp32 accumulators).  K advances
-// in steps of 64 through double-buffered LDS (x tile and dequantised weight tile, rows
-// padded to 72 halves: 144 KB): the next step's global loads are issued before the
-// current step's MFMAs, its weight tile is dequantised and both tiles are written to
-// the other buffer after them, one barrier per step.  All global traffic uses buffer
-// resources, so rows past M or N read as zero and stores past them are dropped; the
-// loads of the step after the last one are harmless and never consumed.
-//
-// Weight dequant, two threads per weight row (16 of the step's 32 quant bytes each):
-// the nibbles are masked into the two halves of a dword as fp16 denormals q*2^-24
-// (or 16q*2^-24 for high nibbles), and v_fma_mix{lo,hi}_f16 computes
-// RN16((d*sc*2^24[/16]) * that - dmin*m) in one fused step: the exact fp32 weight
-// rounded once to fp16.
-constexpr int QBK = 64, QLD = 72;
-
-// MI x NI: 32x32 MFMA tiles per wave; the 8 waves sit as 2 (x rows) x 4 (weight rows),
-// so a workgroup tile is QBM = 64*MI x QBN = 128*NI.
-template <int MI, int NI, typename YT>
-__global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, YT* y, int N, int nsb) {
-  constexpr int QBM = 64 * MI, QBN = 128 * NI, AC = QBM / 64;   // AC: x chunks per thread
-  __shared__ __attribute__((aligned(16))) f16 As[2][QBM][QLD];
-  __shared__ __attribute__((aligned(16))) f16 Bs[2][QBN][QLD];
-  // nsb > 0: split K — this workgroup (blockIdx.z) covers super-blocks
-  // [z*nsb, (z+1)*nsb) and writes its fp32 partial tile to slice z of y
-  const int K = a.K, KT = nsb > 0 ? 4 * nsb : K / QBK;
-  const uint32_t kb = nsb > 0 ? (uint32_t)blockIdx.z * (uint32_t)nsb : 0u;
-  if (nsb > 0) y += (size_t)blockIdx.z * (size_t)M * (size_t)N;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int wm = wave >> 2, wn = wave & 3;
-  const int m0 = (int)blockIdx.y * QBM, n0 = (int)blockIdx.x * QBN;
-  const uint32_t rb = (uint32_t)a.rb;
-  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)x, (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), ALLOY_RSRC_DW3);
-  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)a.w, (short)0, (int)((uint32_t)N * rb), ALLOY_RSRC_DW3);
-  // x tile: QBM rows x 8 chunks of 16 B, AC chunks per thread (8 lanes per row)
-  uint32_t xoff[AC];
-  int arow[AC], acol[AC];
-#pragma unroll
-  for (int i = 0; i < AC; ++i) {
-    const int c = tid + 512 * i;
-    arow[i] = c >> 3;
-    acol[i] = (c & 7) * 8;
-    xoff[i] = ((uint32_t)(m0 + arow[i]) * (uint32_t)K + 256u * kb + (uint32_t)acol[i]) * 2u;
-  }
-  // weight tile: row br; thread half bh owns quant bytes 32p + 16bh .. +15 of every
-  // pair p, i.e. elements 16bh + [0,16) (low nibbles, sub-block 2p) and
-  // 32 + 16bh + [0,16) (high nibbles, sub-block 2p+1) of step p of a super-block.
-  // A thread loads its 80 bytes of a super-block (header + 4 x 16 quant bytes) in one
-  // burst every four steps, so each weight line is fetched into L1 once.  With
-  // QBN = 128 the upper half of the threads mirror the lower half's rows.
-  const int br = (tid >> 1) & (QBN - 1), bh = tid & 1;
-  const uint32_t wrow = (uint32_t)(n0 + br) * rb + 144u * kb;
-
-  struct Blk { u32x4 hd, q[4]; };          // this thread's bytes of one super-block
-  // the super-block / step offsets are uniform: scalar operands of the loads
-  auto bload = [&](int sb, Blk& r) {       // past the end: in-bounds garbage or zeros
-    const uint32_t so = (uint32_t)sb * 144u;
-    r.hd = __builtin_amdgcn_raw_buffer_load_b128(wr, wrow, so, 0);
-#pragma unroll
-    for (int p = 0; p < 4; ++p)
-      r.q[p] = __builtin_amdgcn_raw_buffer_load_b128(wr, wrow + 16u + 32u * p + 16u * (uint32_t)bh, so, 0);
-  };
-  u32x4 xs[AC];                            // x chunks of the next step
-  auto xload = [&](int kt) {
-    const uint32_t so = 2u * (uint32_t)kt * QBK;
-#pragma unroll
-    for (int i = 0; i < AC; ++i) xs[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[i], so, 0);
-  };
-  auto astore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < AC; ++i) *(u32x4*)&As[buf][arow[i]][acol[i]] = xs[i];
-  };
-  // scales/offsets of sub-blocks 2p (low nibbles) and 2p+1 (high) of pair p; the
-  // nibble halves enter v_fma_mix as fp16 denormals q*2^-24 (16q*2^-24 high).  The two
-  // threads of a row (lanes 2i, 2i+1) each decode sub-block 2p+bh and swap the result
-  // with a DPP quad permutation [1,0,3,2].
-  const float smul = bh ? 1048576.f : 16777216.f;      // 2^24 / 16 (high), 2^24 (low)
-  auto swap_pair = [](float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-  };
-  auto scales = [&](const Blk& r, int p, float (&s)[2], float (&c)[2]) {
-    uint32_t sc, mn;
-    q4k_scale_min(r.hd.y, r.hd.z, r.hd.w, 2 * p + bh, sc, mn);   // 2p+bh < 4 iff p < 2
-    const float d = h2f(r.hd.x), dmin = h2f(r.hd.x >> 16);
-    const float so = d * (float)sc * smul, co = -(dmin * (float)mn);
-    const float sp = swap_pair(so), cp = swap_pair(co);
-    s[0] = bh ? sp : so;
-    s[1] = bh ? so : sp;
-    c[0] = bh ? cp : co;
-    c[1] = bh ? co : cp;
-  };
-  // quarter j of a step's dequant: word j of the pair -> 4 elements of each sub-block
-  auto deq = [&](const u32x4& q, int j, const float (&s)[2], const float (&c)[2], int buf) {
-    const uint32_t w = j == 0 ? q.x : j == 1 ? q.y : j == 2 ? q.z : q.w;
-    const uint32_t w8 = w >> 8;
-    uint32_t o[2][2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t m = h ? 0x00F000F0u : 0x000F000Fu;
-      const uint32_t ea = w & m, eb = w8 & m;                 // (e0, e2), (e1, e3)
-      o[h][0] = mix_hi(mix_lo(ea, s[h], c[h]), eb, s[h], c[h]);
-      o[h][1] = mix_hi_h(mix_lo_h(ea, s[h], c[h]), eb, s[h], c[h]);
-    }
-    // elements 16bh + 4j + [0,4) and 32 + 16bh + 4j + [0,4)
-    *(uint2*)&Bs[buf][br][16 * bh + 4 * j] = uint2{o[0][0], o[0][1]};
-    *(uint2*)&Bs[buf][br][32 + 16 * bh + 4 * j] = uint2{o[1][0], o[1][1]};
-  };
-
-  f32x16 acc[MI][NI];
-#pragma unroll
-  for (int i = 0; i < MI; ++i)
-#pragma unroll
-    for (int j = 0; j < NI; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-
-  // Step kt multiplies from LDS buffer kt%2 while step kt+1 is dequantised into the
-  // other buffer in quarters between its MFMA groups and the x chunks of step kt+1
-  // (loaded during step kt-1) are stored; super-block raw bytes are loaded four
-  // steps before their first use.  nb: the super-block holding step kt+1's pair.
-  auto step = [&](int kt, const Blk& nb, int np) {
-    const int cur = kt & 1;
-    float s[2], c[2];
-    scales(nb, np, s, c);
-    const u32x4 q = nb.q[np];
-    u32x4 xk[AC];
-#pragma unroll
-    for (int i = 0; i < AC; ++i) xk[i] = xs[i];
-    xload(kt + 2);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int kc = 16 * ks + 8 * (lane >> 5);
-      f16x8 af[MI], bf[NI];
-#pragma unroll
-      for (int i = 0; i < MI; ++i) af[i] = *(const f16x8*)&As[cur][32 * MI * wm + 32 * i + (lane & 31)][kc];
-#pragma unroll
-      for (int j = 0; j < NI; ++j) bf[j] = *(const f16x8*)&Bs[cur][32 * NI * wn + 32 * j + (lane & 31)][kc];
-#pragma unroll
-      for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int j = 0; j < NI; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-      deq(q, ks, s, c, cur ^ 1);
-      // keep the last MFMAs' operands live across the dequant: its v_fma_mix results
-      // come from inline asm, which the hazard recognizer does not check against
-      // MFMAs still reading their source registers, so they must not reuse those
-      asm volatile("" ::"v"(af[MI - 1]));
-#pragma unroll
-      for (int j = 0; j < NI; ++j) asm volatile("" ::"v"(bf[j]));
-    }
-#pragma unroll
-    for (int i = 0; i < AC; ++i) *(u32x4*)&As[cur ^ 1][arow[i]][acol[i]] = xk[i];
-    __syncthreads();
-  };
-
-  Blk b0, b1;
-  bload(0, b0);
-  bload(1, b1);
-  xload(0);
-  {
-    float s[2], c[2];
-    scales(b0, 0, s, c);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) deq(b0.q[0], j, s, c, 0);
-    astore(0);
-  }
-  xload(1);
-  __syncthreads();
-  // super-blocks in pairs: steps 4S..4S+3 use b0 (pairs 1..3 of S) then b1 (pair 0
-  // of S+1); b0 is reloaded with S+2 once its last pair has been dequantised
-  const int SB = KT / 4;
-  int S = 0;
-  for (; S + 1 < SB; S += 2) {
-    const int kt = 4 * S;
-    step(kt, b0, 1);
-    step(kt + 1, b0, 2);
-    step(kt + 2, b0, 3);
-    bload(S + 2, b0);
-    step(kt + 3, b1, 0);
-    step(kt + 4, b1, 1);
-    step(kt + 5, b1, 2);
-    step(kt + 6, b1, 3);
-    bload(S + 3, b1);
-    step(kt + 7, b0, 0);
-  }
-  if (S < SB) {                            // last super-block (odd count)
-    const int kt = 4 * S;
-    step(kt, b0, 1);
-    step(kt + 1, b0, 2);
-    step(kt + 2, b0, 3);
-    step(kt + 3, b1, 0);                   // dequantises garbage into an unused buffer
-  }
-  // D[i][j] of a tile: j = lane%32 (weight row), i = 8(t/4) + 4(lane/32) + t%4 (x row)
-  constexpr uint32_t esz = sizeof(YT);
-  const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)y, (short)0, (int)((uint32_t)M * (uint32_t)N * esz), ALLOY_RSRC_DW3);
-#pragma unroll
-  for (int i = 0; i < MI; ++i)
-#pragma unroll
-    for (int j = 0; j < NI; ++j) {
-      const int n = n0 + 32 * NI * wn + 32 * j + (lane & 31);
-#pragma unroll
-      for (int t = 0; t < 16; ++t) {
-        const int m = m0 + 32 * MI * wm + 32 * i + 8 * (t >> 2) + 4 * (lane >> 5) + (t & 3);
-        const uint32_t off = n < N ? ((uint32_t)m * (uint32_t)N + (uint32_t)n) * esz : 0x80000000u;
-        // copy the element out first: a bit_cast applied to the vector element
-        // directly picked element 0 for every t in this compiler
-        const float v = acc[i][j][t];
-        if constexpr (sizeof(YT) == 4)
-          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), yr, off, 0, 0);
-        else
-          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (f16)v), yr, off, 0, 0);
-      }
-    }
-}
-
 // ------------------------------------------------------------------ M <= 16 GEMV, Q4_K, 4x4x4 MFMA
 // A wave owns 64 weight rows (one per lane) and a fixed range of SPW super-blocks of
 // K; the W waves of a workgroup cover all of K for the same 64 rows and are reduced
@@ -899,6 +584,7 @@ __global__ __launch_bounds__((m4_max_threads<TG, SPW>())) void k_gemv_q4k_m4(QAr
   }
 }
 
+// ------------------------------------------------------------------ host launchers
 template <template <class> class Fn, typename... Args>
 static hipError_t by_fmt(int fmt, Args&&... args) {
   switch (fmt) {
@@ -1526,135 +1212,6 @@ hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, 
     (void)hipGetLastError();
   }
   return by_fmt<GemvMfmaRun>(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
-}
-
-// Sum of the S fp32 split-K partial slices, in slice order (deterministic).
-template <typename YT>
-__global__ __launch_bounds__(256) void k_splitk_sum(const float* ws, int S, int64_t mn, YT* y) {
-  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
-  if (i >= mn) return;
-  f32x4 acc = *(const f32x4*)(ws + i);
-  for (int z = 1; z < S; ++z) acc += *(const f32x4*)(ws + (int64_t)z * mn + i);
-  if constexpr (sizeof(YT) == 4) {
-    *(f32x4*)((float*)y + i) = acc;
-  } else {
-    const float a0 = acc[0], a1 = acc[1], a2 = acc[2], a3 = acc[3];   // elements copied out first
-    *(f16x4*)((f16*)y + i) = f16x4{(f16)a0, (f16)a1, (f16)a2, (f16)a3};
-  }
-}
-
-// Q4_K GEMM plan: tile kind (0 = 256x256, 1 = 128x256, 2 = 128x128, 3 = 64x256,
-// 4 = 64x128; 5 = 256x256 and 6 = 256x128 with one wave per SIMD, gemm_q4k.hip) and
-// K splits S.  Each kind's measured full-chip rate (TFLOP/s on MI355X) is scaled by
-// the fraction of CU slots its tile count x S fills in the last round of workgroups; a
-// split adds the partial-sum pass ((S+1) fp32 M x N tiles of HBM traffic) and one
-// launch.  S divides the super-blocks, at least two per split.  Kinds 5 and 6 are
-// not planned (rate 0; forced variants 9 / 10 only): measured in the same run, kind 5
-// is 2-12 % below kind 0 on the same tile and kind 6 3-8 % below kind 1 at every shape
-// and split count of the prefill configurations.
-struct GemmPlan { int kind, splits; };
-static GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K, bool allow_split) {
-  const int cus = xs_cu_count();
-  const int bm[7] = {256, 128, 128, 64, 64, 256, 256}, bn[7] = {256, 256, 128, 256, 128, 256, 128};
-  const double rate[7] = {1000e12, 790e12, 600e12, 590e12, 420e12, 0, 0};
-  const double flops = 2.0 * (double)M * (double)N * (double)K;
-  const int64_t sb = K / 256;
-  GemmPlan best{0, 1};
-  double best_t = 1e30;
-  for (int k = 0; k < 7; ++k) {
-    if (rate[k] <= 0) continue;
-    const int64_t tl = ((M + bm[k] - 1) / bm[k]) * ((N + bn[k] - 1) / bn[k]);
-    for (int S = 1; S <= (allow_split ? 4 : 1); ++S) {
-      if (S > 1 && (sb % S || sb / S < 2)) continue;
-      const int64_t wg = tl * S, rounds = (wg + cus - 1) / cus;
-      double t = flops / (rate[k] * (double)wg / (double)(rounds * cus));
-      if (S > 1) t += (double)(S + 1) * (double)M * (double)N * 4.0 / 5e12 + 2e-6;
-      if (t < best_t) { best_t = t; best = GemmPlan{k, S}; }
-    }
-  }
-  return best;
-}
-
-static bool gemm_q4k_fits(int64_t M, int64_t N, const QArgs& a) {   // 32-bit buffer offsets
-  return (uint64_t)M * (uint64_t)a.K * 2u < (1ull << 31) && (uint64_t)N * (uint64_t)a.rb < (1ull << 31) &&
-         (uint64_t)M * (uint64_t)N * 4u < (1ull << 31);
-}
-
-int64_t gemm_workspace_bytes(int fmt, int64_t M, int64_t N, int64_t K) {
-  if (fmt != F_Q4_K || M <= 64 || K % 256) return 0;
-  const GemmPlan p = gemm_plan(M, N, K, true);
-  return p.splits > 1 ? (int64_t)p.splits * M * N * 4 : 0;
-}
-
-template <class F>
-struct GemmRun {
-  static hipError_t run(const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32, int64_t M,
-                        int64_t N, const Opts& o, void* ws, int64_t ws_bytes, hipStream_t st) {
-    if constexpr (std::is_same<F, FQ4K>::value) {
-      if (!x_f32 && gemm_q4k_fits(M, N, a) && (M > 64 || o.variant >= 4) && o.variant != 1) {
-        GemmPlan p = o.variant >= 4 ? GemmPlan{o.variant - 4, 1} : gemm_plan(M, N, a.K, ws != nullptr);
-        if (o.variant >= 4 && o.splits > 1 && (a.K / 256) % o.splits == 0 && a.K / 256 / o.splits >= 2)
-          p.splits = o.splits;             // forced split (falls back to none without the workspace)
-        if (p.splits > 1 &&
-            (ws_bytes < (int64_t)p.splits * M * N * 4 || ((uintptr_t)ws & 15) || ((uintptr_t)y & 15) || (M * N) % 4))
-          p = o.variant >= 4 ? GemmPlan{p.kind, 1} : gemm_plan(M, N, a.K, false);
-        const int nsb = p.splits > 1 ? (int)(a.K / 256 / p.splits) : 0;
-        auto sum_splits = [&]() {
-          const int64_t mn = M * N, blocks = (mn / 4 + 255) / 256;
-          if (y_f32)
-            hipLaunchKernelGGL(k_splitk_sum<float>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)ws,
-                               p.splits, mn, (float*)y);
-          else
-            hipLaunchKernelGGL(k_splitk_sum<f16>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)ws,
-                               p.splits, mn, (f16*)y);
-          return hipGetLastError();
-        };
-        if (p.kind >= 5) {                 // one wave per SIMD (gemm_q4k.hip)
-          const bool split = p.splits > 1;
-          hipError_t e = launch_gemm_q4k_w4(p.kind - 5, a, (const f16*)x, (int)M, split ? ws : y, split || y_f32,
-                                            (int)N, p.splits, nsb, st);
-          return e != hipSuccess || !split ? e : sum_splits();
-        }
-        auto go = [&](auto mi, auto ni) {
-          constexpr int MI = decltype(mi)::value, NI = decltype(ni)::value;
-          const dim3 grid((unsigned)((N + 128 * NI - 1) / (128 * NI)), (unsigned)((M + 64 * MI - 1) / (64 * MI)),
-                          (unsigned)p.splits);
-          if (p.splits > 1)
-            hipLaunchKernelGGL((k_gemm_q4k<MI, NI, float>), grid, dim3(512), 0, st, a, (const f16*)x, (int)M,
-                               (float*)ws, (int)N, nsb);
-          else if (y_f32)
-            hipLaunchKernelGGL((k_gemm_q4k<MI, NI, float>), grid, dim3(512), 0, st, a, (const f16*)x, (int)M,
-                               (float*)y, (int)N, 0);
-          else
-            hipLaunchKernelGGL((k_gemm_q4k<MI, NI, f16>), grid, dim3(512), 0, st, a, (const f16*)x, (int)M,
-                               (f16*)y, (int)N, 0);
-          hipError_t e = hipGetLastError();
-          return e != hipSuccess || p.splits == 1 ? e : sum_splits();
-        };
-        switch (p.kind) {
-          case 0: return go(std::integral_constant<int, 4>(), std::integral_constant<int, 2>());
-          case 1: return go(std::integral_constant<int, 2>(), std::integral_constant<int, 2>());
-          case 3: return go(std::integral_constant<int, 1>(), std::integral_constant<int, 2>());
-          case 4: return go(std::integral_constant<int, 1>(), std::integral_constant<int, 1>());
-          default: return go(std::integral_constant<int, 2>(), std::integral_constant<int, 1>());
-        }
-      }
-    }
-    (void)ws;
-    (void)ws_bytes;
-    dim3 grid((unsigned)((N + GBN - 1) / GBN), (unsigned)((M + GBM - 1) / GBM));
-    if (x_f32)
-      hipLaunchKernelGGL((k_gemm<F, float>), grid, dim3(256), 0, st, a, (const float*)x, (int)M, y, (int)y_f32, N);
-    else
-      hipLaunchKernelGGL((k_gemm<F, f16>), grid, dim3(256), 0, st, a, (const f16*)x, (int)M, y, (int)y_f32, N);
-    return hipGetLastError();
-  }
-};
-
-hipError_t launch_gemm(int fmt, const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32,
-                       int64_t M, int64_t N, const Opts& o, void* ws, int64_t ws_bytes, hipStream_t st) {
-  if (M == 0 || N == 0) return hipSuccess;
-  return by_fmt<GemmRun>(fmt, a, x, x_f32, y, y_f32, M, N, o, ws, ws_bytes, st);
 }
 
 }  // namespace alloy

@@ -36,6 +36,23 @@ __device__ __forceinline__ void lds_barrier_asm() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// y[i] = v as fp32 or RN16
+__device__ __forceinline__ void store_y(void* y, bool y_f32, int64_t i, float v) {
+  if (y_f32) ((float*)y)[i] = v;
+  else ((f16*)y)[i] = (f16)v;
+}
+
+// elements k0..k0+31 of row n as RN16 of their exact fp32 values
+template <class F>
+__device__ __forceinline__ void dec32_f16(const QArgs& a, int64_t n, int k0, f16x8 (&o)[4]) {
+  float w[32];
+  F::dec32(a, n, k0, w);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[j][e] = (f16)w[8 * j + e];   // RNE
+}
+
 template <typename XT>
 __device__ __forceinline__ f16x8 ld_x8(const XT* p);
 template <>
@@ -112,30 +129,6 @@ __device__ __forceinline__ float dpp_sum_rows(float v, int lshift) {
   const float s32 = v + dpp_f<0x142, 0xA>(v);        // row_bcast:15 -> rows 1, 3: 32-lane sums
   const float s64 = s32 + dpp_f<0x143, 0xC>(s32);    // row_bcast:31 -> row 3: 64-lane sum
   return lshift == 4 ? v : lshift == 5 ? s32 : s64;
-}
-
-// Q4_K GEMM dequant: a nibble masked into the low bits of an fp16 half is the
-// denormal q*2^-24 (16q*2^-24 for a high nibble); v_fma_mix multiplies it by the
-// scale (pre-multiplied by 2^24 or 2^20), adds the offset in fp32 and rounds once to
-// fp16.
-// mix_lo* start a dword (the high half is left undefined for a following mix_hi*)
-__device__ __forceinline__ uint32_t mix_lo(uint32_t q, float s, float c) {               // q.lo
-  uint32_t d;
-  asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(q), "v"(s), "v"(c));
-  return d;
-}
-__device__ __forceinline__ uint32_t mix_hi(uint32_t d, uint32_t q, float s, float c) {   // q.lo
-  asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "+v"(d) : "v"(q), "v"(s), "v"(c));
-  return d;
-}
-__device__ __forceinline__ uint32_t mix_lo_h(uint32_t q, float s, float c) {             // q.hi
-  uint32_t d;
-  asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(q), "v"(s), "v"(c));
-  return d;
-}
-__device__ __forceinline__ uint32_t mix_hi_h(uint32_t d, uint32_t q, float s, float c) { // q.hi
-  asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(d) : "v"(q), "v"(s), "v"(c));
-  return d;
 }
 
 }  // namespace alloy

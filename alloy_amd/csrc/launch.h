@@ -63,10 +63,6 @@ hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, 
 hipError_t launch_gemm(int fmt, const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32,
                        int64_t M, int64_t N, const Opts& o, void* ws, int64_t ws_bytes, hipStream_t st);
 int64_t gemm_workspace_bytes(int fmt, int64_t M, int64_t N, int64_t K);
-// Q4_K GEMM with one wave per SIMD (gemm_q4k.hip): kind 0 = 256 x 256 tile, 1 = 256 x 128;
-// splits > 1: fp32 partial tiles of nsb super-blocks each into y (the workspace).
-hipError_t launch_gemm_q4k_w4(int kind, const QArgs& a, const _Float16* x, int M, void* y, bool y_f32, int N,
-                              int splits, int nsb, hipStream_t st);
 
 // Gated pair y = act(x G^T) * (x U^T) (act 0 silu, 1 gelu in tanh form): one fused
 // launch for M <= 16 when glu_fused_supported(), else two products into fp32

@@ -1,20 +1,16 @@
-"""Quantization formats: buffer tables and validation, mirroring the reference.
+"""Weight formats of the quantized-linear path: GGUF wire-block geometry, the buffers
+each drop-in module holds, and their validation.
 
-``QUANT_FORMATS`` follows the reference's table of GGUF formats
-(``packages/alloy-server/src/alloy_server/gguf/quant.py:38-78``): the buffers a
-quantized Linear holds, their dtypes, and column counts as a function of the
-contraction dim.  ``validate_quant_buffers`` / ``validate_mlx_buffers`` raise the
-same exception types for the same conditions as the reference
-(``gguf/quant.py:81-105``; ``packages/alloy-server/src/alloy_server/mlx/quant.py:88-109``).
-
-Wire-block sizes (bytes per block, weights per block) of the GGUF formats are in
-``BLOCK``; ``row_bytes`` gives the bytes of one weight row.
+The buffer sets are the reference modules' interface (names, dtypes and column counts
+of ``packages/alloy-server/src/alloy_server/gguf/quant.py:36-78`` and
+``packages/alloy-server/src/alloy_server/mlx/quant.py:27-59``): Q8_0 and Q5_0 in the
+reference's split layout, Q4_K and Q6_K as raw GGUF rows, MLX 4-bit as uint8 nibbles
+plus fp16 group scales and biases.  The checks keep the reference's exception contract
+(``ValueError`` for a wrong buffer set, shape or divisibility, ``TypeError`` for a
+dtype; ``gguf/quant.py:81-105``, ``mlx/quant.py:88-109``).
 """
 
 from __future__ import annotations
-
-from collections.abc import Callable
-from dataclasses import dataclass
 
 import torch
 
@@ -23,6 +19,7 @@ BLOCK = {"q8_0": (32, 34), "q5_0": (32, 22), "q4_k": (256, 144), "q6_k": (256, 2
 
 
 def row_bytes(fmt: str, K: int) -> int:
+    """Bytes of one weight row of K elements in GGUF wire blocks."""
     qk, bb = BLOCK[fmt]
     if K % qk:
         raise ValueError(f"{fmt}: K={K} not divisible by {qk}")
@@ -38,76 +35,61 @@ def bits_per_weight(fmt: str, group_size: int = 64) -> float:
     raise KeyError(fmt)
 
 
-@dataclass(frozen=True)
-class QuantBuffer:
-    name: str
-    dtype: torch.dtype
-    cols: Callable[[int], int]
+def module_buffers(fmt: str, rows: int, K: int) -> dict[str, tuple[torch.dtype, tuple[int, int]]]:
+    """The buffers (name -> (dtype, shape)) a quantized weight of ``rows`` x ``K`` is held
+    in, in the order the reference op takes them.  K must be a multiple of the block."""
+    if fmt == "q8_0":
+        return {"qweight": (torch.int8, (rows, K)), "scales": (torch.float16, (rows, K // 32))}
+    if fmt == "q5_0":
+        half = (rows, K // 2)
+        return {"qweight": (torch.uint8, half), "qhigh": (torch.uint8, half),
+                "scales": (torch.float16, (rows, K // 32))}
+    if fmt == "q4_k":
+        return {"blocks": (torch.uint8, (rows, row_bytes(fmt, K)))}
+    if fmt == "q6_k":
+        return {"qweight": (torch.uint8, (rows, row_bytes(fmt, K)))}
+    raise KeyError(fmt)
 
 
-@dataclass(frozen=True)
-class QuantFormat:
-    name: str
-    align: int
-    buffers: tuple[QuantBuffer, ...]
-
-    @property
-    def buffer_names(self) -> tuple[str, ...]:
-        return tuple(b.name for b in self.buffers)
-
-
-QUANT_FORMATS: dict[str, QuantFormat] = {
-    "q8_0": QuantFormat("q8_0", 32, (
-        QuantBuffer("qweight", torch.int8, lambda k: k),
-        QuantBuffer("scales", torch.float16, lambda k: k // 32),
-    )),
-    "q5_0": QuantFormat("q5_0", 32, (
-        QuantBuffer("qweight", torch.uint8, lambda k: k // 2),
-        QuantBuffer("qhigh", torch.uint8, lambda k: k // 2),
-        QuantBuffer("scales", torch.float16, lambda k: k // 32),
-    )),
-    "q4_k": QuantFormat("q4_k", 256, (
-        QuantBuffer("blocks", torch.uint8, lambda k: (k // 256) * 144),
-    )),
-    "q6_k": QuantFormat("q6_k", 256, (
-        QuantBuffer("qweight", torch.uint8, lambda k: (k // 256) * 210),
-    )),
-}
+def check_module_buffers(fmt: str, buffers: dict[str, torch.Tensor], *, rows: int, K: int, what: str) -> None:
+    """Raise unless ``buffers`` are exactly the ``module_buffers(fmt, rows, K)`` set."""
+    qk = BLOCK[fmt][0]
+    if K % qk:
+        raise ValueError(f"{what}: {fmt} rows of {K} elements are not divisible into blocks of {qk}")
+    want = module_buffers(fmt, rows, K)
+    if set(buffers) != set(want):
+        raise ValueError(f"{what}: a {fmt} weight is held in buffers ({', '.join(want)}), "
+                         f"given ({', '.join(buffers) or 'nothing'})")
+    for name, (dtype, shape) in want.items():
+        t = buffers[name]
+        if t.dtype != dtype:
+            raise TypeError(f"{what}: {fmt} buffer {name} holds {dtype}, given {t.dtype}")
+        if tuple(t.shape) != shape:
+            raise ValueError(f"{what}: {fmt} buffer {name} for {rows} rows of {K} elements is {shape}, "
+                             f"given {tuple(t.shape)}")
 
 
-def validate_quant_buffers(fmt: QuantFormat, buffers: dict[str, torch.Tensor], *, rows: int, dim: int,
-                           kind: str) -> None:
-    if set(buffers) != set(fmt.buffer_names):
-        raise ValueError(f"{fmt.name} {kind} expects buffers {fmt.buffer_names}, got {tuple(buffers)}")
-    if dim % fmt.align != 0:
-        raise ValueError(f"{fmt.name} {kind} dim {dim} not divisible by {fmt.align}")
-    for b in fmt.buffers:
-        t = buffers[b.name]
-        if t.dtype is not b.dtype:
-            raise TypeError(f"{fmt.name} {kind} buffer {b.name!r} requires {b.dtype}, got {t.dtype}")
-        if t.ndim != 2:
-            raise ValueError(f"{fmt.name} {kind} buffer {b.name!r} must be rank-2, got {tuple(t.shape)}")
-        expected = (rows, b.cols(dim))
-        if tuple(t.shape) != expected:
-            raise ValueError(
-                f"{fmt.name} {kind} buffer {b.name!r} shape {tuple(t.shape)} != {expected} (rows={rows} dim={dim})"
-            )
-
-
-def validate_mlx_buffers(qweight: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *, rows: int,
-                         dim: int, kind: str) -> None:
-    if qweight.dtype is not torch.uint8:
-        raise TypeError(f"MLX {kind} qweight must be uint8, got {qweight.dtype}")
-    if scales.dtype is not torch.float16 or biases.dtype is not torch.float16:
-        raise TypeError(f"MLX {kind} scales/biases must be float16")
-    if tuple(qweight.shape) != (rows, dim // 2) or scales.shape != biases.shape or scales.shape[0] != rows:
-        raise ValueError(
-            f"MLX {kind} buffer shapes inconsistent: qweight {tuple(qweight.shape)}, "
-            f"scales {tuple(scales.shape)} (rows={rows} dim={dim})"
-        )
+def check_mlx_buffers(qweight: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *, rows: int, K: int,
+                      what: str) -> int:
+    """Raise unless (qweight, scales, biases) hold ``rows`` x ``K`` MLX 4-bit weights;
+    returns the group size."""
+    if qweight.dtype != torch.uint8:
+        raise TypeError(f"{what}: MLX qweight holds uint8 nibble pairs, given {qweight.dtype}")
+    for name, t in (("scales", scales), ("biases", biases)):
+        if t.dtype != torch.float16:
+            raise TypeError(f"{what}: MLX {name} are float16, given {t.dtype}")
+    if K % 2 or tuple(qweight.shape) != (rows, K // 2):
+        raise ValueError(f"{what}: MLX qweight for {rows} rows of {K} elements is ({rows}, {K // 2}), "
+                         f"given {tuple(qweight.shape)}")
+    if scales.ndim != 2 or scales.shape[0] != rows or tuple(biases.shape) != tuple(scales.shape):
+        raise ValueError(f"{what}: MLX scales {tuple(scales.shape)} and biases {tuple(biases.shape)} "
+                         f"must both be ({rows}, groups)")
     groups = scales.shape[1]
-    if groups == 0 or dim % groups != 0 or (dim // groups) % 8 != 0:
-        raise ValueError(f"MLX {kind} group size {dim}/{groups} unsupported (must divide dim, multiple of 8)")
+    gs = K // groups if groups else 0
+    if groups == 0 or gs * groups != K or gs % 8:
+        raise ValueError(f"{what}: {K} elements in {groups} MLX groups is not a whole group size "
+                         f"that is a multiple of 8")
+    return gs
 
 
 def mlx_group_size(qweight: torch.Tensor, scales: torch.Tensor) -> int:
@@ -117,6 +99,6 @@ def mlx_group_size(qweight: torch.Tensor, scales: torch.Tensor) -> int:
 
 
 def mlx_qweight_to_uint8(weight: torch.Tensor) -> torch.Tensor:
-    """MLX packed uint32 weight [N, K/8] -> uint8 [N, K/2], a little-endian
-    reinterpret (``packages/alloy-server/src/alloy_server/mlx/quant.py:20-24``)."""
+    """MLX packed uint32 weight [N, K/8] -> uint8 [N, K/2]: the little-endian bytes of
+    each word, low nibble first (``packages/alloy-server/src/alloy_server/mlx/quant.py:20-24``)."""
     return weight.contiguous().view(torch.uint8)

@@ -124,7 +124,7 @@ class GGUFFile:
         return torch.from_numpy(np.array(a).reshape(t.shape))
 
     def quant_buffers(self, name: str, *, split: bool = True) -> dict[str, torch.Tensor]:
-        """Host tensors named as the quantized modules' buffers (``formats.QUANT_FORMATS``):
+        """Host tensors named as the quantized modules' buffers (``formats.module_buffers``):
         q4_k ``blocks``; q6_k ``qweight``; q8_0 ``qweight``/``scales`` and q5_0
         ``qweight``/``qhigh``/``scales`` in the reference's split layout, or the wire
         ``blocks`` (for ``gguf_q8_0_blocks_mm`` / ``gguf_q5_0_blocks_mm``) with

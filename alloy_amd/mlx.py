@@ -1,11 +1,11 @@
 """MLX 4-bit safetensors checkpoints to the buffers of ``MLXQ4Linear`` / ``MLXQ4Embedding``.
 
-Follows the reference's tensor scan (``packages/alloy-server/src/alloy_server/mlx/
-loader.py:58-110``): a tensor ``<base>.weight`` is quantized when ``<base>.scales``
-exists; its packed uint32 ``[N, K/8]`` weight is reinterpreted as uint8 ``[N, K/2]``
-(``mlx_qweight_to_uint8``), and ``.scales`` / ``.biases`` are converted to float16.
-Every other tensor is dense (floating tensors converted to ``dense_dtype``).  Only
-4-bit checkpoints are accepted (``loader.py:60-63``).
+The checkpoint convention (the one ``packages/alloy-server/src/alloy_server/mlx/
+loader.py:58-110`` reads): a quantized weight is stored as ``<base>.weight`` (packed
+uint32 ``[N, K/8]``, eight nibbles per word, low first) with ``<base>.scales`` and
+``<base>.biases`` beside it; every other tensor is dense.  Here the packed words are
+viewed as uint8 ``[N, K/2]`` (``mlx_qweight_to_uint8``), scales and biases become
+float16, dense floating tensors ``dense_dtype``; only 4-bit checkpoints are accepted.
 """
 
 from __future__ import annotations
@@ -16,7 +16,7 @@ from pathlib import Path
 
 import torch
 
-from .formats import mlx_group_size, mlx_qweight_to_uint8, validate_mlx_buffers
+from .formats import check_mlx_buffers, mlx_group_size, mlx_qweight_to_uint8
 
 WEIGHT_SUFFIX = ".weight"
 
@@ -48,39 +48,38 @@ class MLXCheckpoint:
 
 def read_mlx_checkpoint(shards: list[str | Path], config: dict | None = None, *,
                         dense_dtype: torch.dtype = torch.float32) -> MLXCheckpoint:
-    """Read MLX safetensors shards.  ``config`` (the model's config.json) is checked to be
-    a 4-bit quantization when given."""
+    """Read MLX safetensors shards.  ``config`` (the model's config.json), when given,
+    must declare a 4-bit quantization (``NotImplementedError`` for other widths,
+    ``ValueError`` for none)."""
     from safetensors import safe_open
 
     if config is not None:
         quant = mlx_quantization(config)
         if quant is None:
-            raise ValueError("not an MLX-quantized model")
+            raise ValueError("config.json declares no MLX quantization")
         if int(quant.get("bits", 0)) != 4:
-            raise NotImplementedError(f"only MLX 4-bit is supported, got {quant}")
-    out = MLXCheckpoint()
+            raise NotImplementedError(f"MLX checkpoints of {quant.get('bits')} bits are not supported (4 only)")
+    ckpt = MLXCheckpoint()
     with ExitStack() as stack:
-        index = {}
-        for shard in shards:
-            h = stack.enter_context(safe_open(str(shard), framework="pt"))
-            for key in h.keys():
-                index[key] = h
-        bases = {k[:-len(WEIGHT_SUFFIX)] for k in index
-                 if k.endswith(WEIGHT_SUFFIX) and k[:-len(WEIGHT_SUFFIX)] + ".scales" in index}
-        for key, h in index.items():
-            if key.endswith((".scales", ".biases")):
-                continue
-            base = key[:-len(WEIGHT_SUFFIX)] if key.endswith(WEIGHT_SUFFIX) else None
-            if base is not None and base in bases:
-                q = mlx_qweight_to_uint8(h.get_tensor(key))
-                s = index[base + ".scales"].get_tensor(base + ".scales").to(torch.float16)
-                b = index[base + ".biases"].get_tensor(base + ".biases").to(torch.float16)
-                validate_mlx_buffers(q, s, b, rows=q.shape[0], dim=q.shape[1] * 2, kind=base)
-                gs = mlx_group_size(q, s)
-                if out.group_size is None:
-                    out.group_size = gs
-                out.quantized[base] = {"qweight": q, "scales": s, "biases": b}
-            else:
-                t = h.get_tensor(key)
-                out.dense[key] = t.to(dense_dtype) if t.is_floating_point() else t
-    return out
+        handles = [stack.enter_context(safe_open(str(p), framework="pt")) for p in shards]
+        where = {key: h for h in handles for key in h.keys()}      # tensor name -> its shard
+
+        def load(key: str) -> torch.Tensor:
+            return where[key].get_tensor(key)
+
+        # a quantized weight is the triple <base>.weight / .scales / .biases
+        triples = {key[: -len(".scales")] for key in where if key.endswith(".scales")}
+        triples = {b for b in triples if b + WEIGHT_SUFFIX in where}
+        for base in sorted(triples):
+            if base + ".biases" not in where:
+                raise ValueError(f"MLX tensor {base} has scales but no biases")
+            qweight = mlx_qweight_to_uint8(load(base + WEIGHT_SUFFIX))
+            scales, biases = load(base + ".scales").half(), load(base + ".biases").half()
+            check_mlx_buffers(qweight, scales, biases, rows=qweight.shape[0], K=2 * qweight.shape[1], what=base)
+            ckpt.group_size = ckpt.group_size or mlx_group_size(qweight, scales)
+            ckpt.quantized[base] = {"qweight": qweight, "scales": scales, "biases": biases}
+        owned = {base + sfx for base in triples for sfx in (WEIGHT_SUFFIX, ".scales", ".biases")}
+        for key in where.keys() - owned:
+            t = load(key)
+            ckpt.dense[key] = t.to(dense_dtype) if t.is_floating_point() else t
+    return ckpt

@@ -9,7 +9,9 @@
  *
  * Conventions
  *   - Every pointer is a DEVICE pointer owned by the caller; the library never
- *     allocates memory and never keeps state between calls.
+ *     allocates device memory.  Its only state is a per-process cache of device
+ *     attributes (CU count per device, kernel occupancy per kernel), filled on first
+ *     use under atomics; results never depend on earlier calls.
  *   - `stream` is a hipStream_t (NULL = default stream); all work is enqueued on
  *     it, asynchronously.  Calls are reentrant; concurrent calls on different
  *     streams do not interact.
@@ -85,9 +87,9 @@ typedef enum {
  *   with the weights dequantised to fp16 before the MFMA (Q4_K, Q6_K, MLX), 9 the
  *   LDS-staged rows of variant 4 for up to 8 rows of x.  GEMM: 1 generic
  *   128x128 tiles, 4 / 5 / 6 / 7 / 8 Q4_K tiles of 256x256 / 128x256 / 128x128 /
- *   64x256 / 64x128, 9 / 10 Q4_K tiles of 256x256 / 256x128 with one wave per SIMD;
- *   bits 40-43 K splits for such a forced Q4_K tile (dividing K/256 with at least
- *   two super-blocks each; needs a workspace of splits*M*N*4 bytes, else unsplit).
+ *   64x256 / 64x128; bits 40-43 K splits for such a forced Q4_K tile (dividing K/256
+ *   with at least two super-blocks each; needs a workspace of splits*M*N*4 bytes,
+ *   else unsplit).
  * No reference counterpart as a single op: the reference dispatches per format
  * (packages/alloy-torch/src/alloy_torch/ops/linalg.py:346-739); the named entry
  * points below are the per-op replacements and all route here.

@@ -224,7 +224,7 @@ def test_mlx_checkpoint_reader(tmp_path):
     assert type(emb) is MLXQ4Embedding and emb.embedding_dim == K
     head = tied_output_head(emb)
     assert type(head) is MLXQ4Linear and head.qweight.data_ptr() == emb.qweight.data_ptr()
-    with pytest.raises(TypeError, match="Linear output head"):
+    with pytest.raises(TypeError, match="replaces an nn.Linear"):
         tied_output_head(emb, torch.nn.Identity())
     with pytest.raises(NotImplementedError):
         mlx.read_mlx_checkpoint(shards, {"quantization": {"group_size": gs, "bits": 8}})

@@ -171,11 +171,26 @@ def test_gemm(dev, fmt, M, N, K):
     y = wt.qmm(xt, path="gemm", out_dtype=torch.float32).cpu().numpy()
     check(y, x, wt.W, f"{fmt} gemm M={M} N={N} K={K}")
     if fmt == "q4_k":
-        # every kernel: 1 = 128x128 generic, 4/5/6 = Q4_K 256x256 / 128x256 / 128x128 tiles,
-        # 9/10 = Q4_K 256x256 / 256x128 tiles with one wave per SIMD
-        for variant in (1, 4, 5, 6, 9, 10):
-            yv = wt.qmm(xt, path="gemm", out_dtype=torch.float32, opts=variant << 36).cpu().numpy()
-            check(yv, x, wt.W, f"{fmt} gemm M={M} N={N} K={K} variant={variant}")
+        # every kernel: 1 = 128x128 generic, 4/5/6/7/8 = Q4_K tiles of 256x256 / 128x256 /
+        # 128x128 / 64x256 / 64x128
+        for variant in (1, 4, 5, 6, 7, 8):
+            yv = wt.qmm(xt, path="gemm", out_dtype=torch.float32, opts=variant << 36)
+            check(yv.cpu().numpy(), x, wt.W, f"{fmt} gemm M={M} N={N} K={K} variant={variant}")
+
+
+@pytest.mark.parametrize("M,N,K", [(130, 200, 768), (300, 130, 2816), (65, 257, 256)])
+def test_gemm_q4k_odd_superblocks(dev, M, N, K):
+    """K with an odd number of super-blocks (3, 11, 1): the kernel's 12-step loop ends
+    with a 4- or 8-step tail, or runs the tail alone; every Q4_K tile."""
+    rng = np.random.default_rng(M + K)
+    wt = Weight("q4_k", N, K, rng, dev)
+    x = synth.numpy_x(M, K, rng)
+    xt = torch.from_numpy(x).to(dev)
+    for variant in (4, 5, 6, 7, 8):
+        yv = wt.qmm(xt, path="gemm", out_dtype=torch.float32, opts=variant << 36)
+        check(yv.cpu().numpy(), x, wt.W, f"gemm K={K} variant={variant}")
+    yd = wt.qmm(xt, path="gemm", out_dtype=torch.float32)
+    check(yd.cpu().numpy(), x, wt.W, f"gemm K={K} default plan")
 
 
 @pytest.mark.parametrize("M,K,N", [(512, 4096, 256), (300, 2048, 130), (512, 14336, 512)])
@@ -201,10 +216,25 @@ def test_gemm_split_k(dev, M, K, N):
     torch.cuda.synchronize()
     check(y1.cpu().numpy(), x, wt.W, "unsplit GEMM (no workspace)")
     # every Q4_K tile with a forced split of 2 and 4
-    for variant in (4, 5, 6, 7, 8, 9, 10):
+    for variant in (4, 5, 6, 7, 8):
         for S in (2, 4):
             yv = wt.qmm(xt, out_dtype=torch.float32, path="gemm", opts=(variant << 36) | (S << 40))
             check(yv.cpu().numpy(), x, wt.W, f"GEMM variant={variant} splits={S}")
+
+
+def test_gemm_split_k_odd_slices(dev):
+    """K splits whose slices hold an odd number of super-blocks (K = 1536: 3 per slice
+    at S = 2, 2 at S = 3): each slice ends in the kernel's 4- or 8-step tail and its
+    prefetches stop at the slice's end."""
+    rng = np.random.default_rng(77)
+    M, N, K = 260, 300, 1536
+    wt = Weight("q4_k", N, K, rng, dev)
+    x = synth.numpy_x(M, K, rng)
+    xt = torch.from_numpy(x).to(dev)
+    for variant in (4, 5, 6, 7, 8):
+        for S in (2, 3):
+            yv = wt.qmm(xt, out_dtype=torch.float32, path="gemm", opts=(variant << 36) | (S << 40))
+            check(yv.cpu().numpy(), x, wt.W, f"GEMM K={K} variant={variant} splits={S}")
 
 
 def test_outputs_deterministic_and_f16(dev):
@@ -266,10 +296,30 @@ def test_q8_0_config1(dev):
     _sampled("q8_0", 4096, 4096, 1, dev, seed=0)
 
 
-@pytest.mark.parametrize("M", [512, 2048])
+@pytest.mark.parametrize("M", [512, 2048, 4096])
 @pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 14336), (14336, 4096)])
 def test_q4_k_prefill_shapes(dev, M, K, N):
     _sampled("q4_k", N, K, M, dev, seed=M + K + N, path="gemm")
+
+
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 14336), (14336, 4096)])
+def test_q4_k_prefill_m4096_op_fp16(dev, K, N):
+    """Config 4 at M = 4096 through the reference's op (fp16 output, the default plan
+    with its workspace), sampled weight rows against the oracle."""
+    M, seed = 4096, 5 * K + N
+    w = synth.torch_blocks("q4_k", N, K, seed, dev)
+    x = synth.torch_x(M, K, seed + 1, dev)
+    y = torch.ops.alloy.gguf_q4_k_mm(x, w)
+    assert y.dtype == torch.float16 and y.shape == (M, N)
+    rng = np.random.default_rng(seed)
+    rows = np.unique(np.concatenate([rng.integers(0, N, 48), [0, N - 1]]))
+    W = oq.dequant("q4_k", w[torch.from_numpy(rows).to(dev)].cpu().numpy(), K)
+    check(y.float().cpu().numpy()[:, rows], x.cpu().numpy(), W, f"gguf_q4_k_mm M={M} K={K} N={N}")
+
+
+def test_q4_k_prefill_k11008(dev):
+    # 43 super-blocks per row (odd), a real prefill width (Llama-2-7B down projection)
+    _sampled("q4_k", 1000, 11008, 700, dev, seed=11008, path="gemm")
 
 
 @pytest.mark.parametrize("gs", [32, 128, 256])

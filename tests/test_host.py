@@ -108,14 +108,14 @@ def test_ops_refuse_cpu_tensors():
 
 
 def test_module_validation_matches_reference():
-    with pytest.raises(ValueError, match="not divisible"):
+    with pytest.raises(ValueError, match="not divisible into blocks"):
         GGUFQ4_KLinear(in_features=100, out_features=2, blocks=torch.zeros((2, 144), dtype=torch.uint8))
     with pytest.raises(TypeError):
         GGUFQ8_0Linear(in_features=64, out_features=2, qweight=torch.zeros((2, 64), dtype=torch.uint8),
                        scales=torch.zeros((2, 2), dtype=torch.float16))
-    with pytest.raises(ValueError, match="expects buffers"):
+    with pytest.raises(ValueError, match="is held in buffers"):
         GGUFQ8_0Linear(in_features=64, out_features=2, qweight=torch.zeros((2, 64), dtype=torch.int8))
-    with pytest.raises(ValueError, match="group size"):
+    with pytest.raises(ValueError, match="not a whole group size"):
         MLXQ4Linear(in_features=64, out_features=2, qweight=torch.zeros((2, 32), dtype=torch.uint8),
                     scales=torch.zeros((2, 3), dtype=torch.float16), biases=torch.zeros((2, 3), dtype=torch.float16))
     m = GGUFQ4_KLinear(in_features=512, out_features=3, blocks=torch.zeros((3, 288), dtype=torch.uint8))
@@ -151,13 +151,13 @@ def test_gguf_moe_modules_validate_like_reference():
                               down_qweight=torch.zeros((E, H, 210), dtype=torch.uint8), num_experts=E,
                               hidden_size=H, moe_intermediate_size=I)
     assert ok.gate_up_blocks.shape == (E, 2 * I, 288)
-    with pytest.raises(RuntimeError, match="weight holder"):
+    with pytest.raises(RuntimeError, match="only holds the expert weights"):
         ok()
-    with pytest.raises(ValueError, match="divisible by 256"):
+    with pytest.raises(ValueError, match="multiples of 256"):
         GGUFQwen35MoeExperts(gate_up_blocks=torch.zeros((E, 2 * 100, 288), dtype=torch.uint8),
                              down_qweight=torch.zeros((E, H, 210), dtype=torch.uint8), num_experts=E,
                              hidden_size=H, moe_intermediate_size=100)
-    with pytest.raises(ValueError, match="do not match"):
+    with pytest.raises(ValueError, match="gate_up_blocks for E=2"):
         GGUFQwen35MoeExperts(gate_up_blocks=torch.zeros((E, I, 288), dtype=torch.uint8),
                              down_qweight=torch.zeros((E, H, 210), dtype=torch.uint8), num_experts=E,
                              hidden_size=H, moe_intermediate_size=I)
