@@ -57,6 +57,7 @@ SIGNATURES = {
     "alloy_moe_workspace_bytes": (_sz, [_i64, _i32, _i32, _i64, _i64]),
     "alloy_mlx_moe_routed": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i64, _i64, _i64, _vp, _sz, _vp, _vp]),
     "alloy_gguf_moe_routed": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i64, _i64, _i64, _vp, _sz, _vp, _vp]),
+    "alloy_gguf_moe_routed_noalloc": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i64, _i64, _i64, _vp, _vp]),
     "alloy_embedding": (_i32, [_i32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _i64, _i64, _i64, _vp, _vp]),
     "alloy_qmm_batched": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp, _i32, _i64, _i64, _vp]),
     "alloy_glu_workspace_bytes": (_sz, [_i32, _i64, _i64, _i64, _i32, _i32]),

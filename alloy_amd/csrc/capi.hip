@@ -3,6 +3,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <string>
 
 #include "../../include/alloy_amd.h"
@@ -433,6 +434,58 @@ alloy_status alloy_gguf_moe_routed(const void* hidden, const float* logits, cons
   m.ws = (uint8_t*)ws;
   m.y = y;
   return hip_status(alloy::launch_gguf_moe(m, L, (hipStream_t)stream), "gguf moe launch");
+}
+
+// ------------------------------------------------------------------ allocation-free MoE
+// The workspace of alloy_gguf_moe_routed_noalloc: a file-scope device array (each GPU
+// the library runs on holds its own copy until the process ends).  Host code never
+// passes `scratch` itself to a kernel (in host code it names a host-side stand-in);
+// it uses the device address hipGetSymbolAddress returns, resolved once per device
+// with that device current.  Every call on one GPU shares the array: calls that
+// overlap (other streams) race and must be serialized by the caller.  The MoE
+// kernels need no zeroed workspace (every region is written before it is read).
+}  // extern "C"
+
+namespace {
+constexpr size_t kMoeScratchBytes = ALLOY_MOE_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) uint8_t scratch[kMoeScratchBytes];
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch[kMaxDevices];
+
+// device address of this GPU's scratch array (device `dev` current), nullptr on failure
+void* scratch_ptr(int dev) {
+  void* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+  g_scratch[dev].store(p, std::memory_order_release);
+  return p;
+}
+}  // namespace
+
+extern "C" {
+
+alloy_status alloy_gguf_moe_routed_noalloc(const void* hidden, const float* logits, const void* gate_up_blocks,
+                                           const void* down_qweight, int32_t E, int32_t top_k, int64_t T,
+                                           int64_t H, int64_t I, float* y, void* stream) {
+  if (T < 0 || E <= 0 || top_k <= 0 || H <= 0 || I <= 0)
+    return alloy_gguf_moe_routed(hidden, logits, gate_up_blocks, down_qweight, E, top_k, T, H, I, nullptr, 0, y,
+                                 stream);   // the argument errors of the workspace entry point
+  if (E <= alloy::kMoeMaxExperts && top_k <= E && top_k <= alloy::kMoeMaxTopK && T * top_k <= alloy::kMoeMaxRoutes) {
+    const size_t need = alloy::moe_layout(T, E, top_k, H, I).total;
+    if (need > kMoeScratchBytes)
+      return fail(ALLOY_E_UNSUPPORTED,
+                  "gguf_moe_routed_noalloc: T=%lld needs %zu workspace bytes, beyond the %zu-byte static scratch",
+                  (long long)T, need, kMoeScratchBytes);
+  }
+  if (T == 0) return alloy_gguf_moe_routed(hidden, logits, gate_up_blocks, down_qweight, E, top_k, T, H, I, nullptr,
+                                           0, y, stream);
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(ALLOY_E_HIP, "gguf_moe_routed_noalloc: no current device (or device index %d >= %d)", dev, kMaxDevices);
+  void* ws = scratch_ptr(dev);
+  if (!ws) return fail(ALLOY_E_HIP, "gguf_moe_routed_noalloc: hipGetSymbolAddress of the scratch array failed");
+  return alloy_gguf_moe_routed(hidden, logits, gate_up_blocks, down_qweight, E, top_k, T, H, I, ws, kMoeScratchBytes,
+                               y, stream);
 }
 
 }  // extern "C"

@@ -279,6 +279,23 @@ alloy_status alloy_gguf_moe_routed(const void* hidden, const float* router_logit
                                    int32_t top_k, int64_t T, int64_t H, int64_t I, void* workspace,
                                    size_t workspace_bytes, float* y, void* stream);
 
+/*
+ * gguf_moe_routed without a workspace argument.  No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same computation, routing and
+ * results as alloy_gguf_moe_routed; the workspace is a library-owned static device
+ * array of ALLOY_MOE_NOALLOC_SCRATCH_BYTES on each GPU (held until the process
+ * ends).  A shape whose alloy_moe_workspace_bytes(T, E, top_k, H, I) exceeds it
+ * returns ALLOY_E_UNSUPPORTED (at H = 2048, I = 768, top_k = 8: T <= 256).  All calls
+ * on one GPU share the array: calls that overlap (other streams) race and must be
+ * serialized by the caller.  Calls no hipMalloc / hipFree.
+ */
+#define ALLOY_MOE_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+alloy_status alloy_gguf_moe_routed_noalloc(const void* hidden, const float* router_logits,
+                                           const void* gate_up_blocks, const void* down_qweight, int32_t E,
+                                           int32_t top_k, int64_t T, int64_t H, int64_t I, float* y,
+                                           void* stream);
+
 /* Thread-local message of the last failed call on this thread ("" if none). */
 const char* alloy_last_error(void);
 /* Library version string. */
