@@ -13,7 +13,9 @@ activation) — TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 Pinning: silu against ``scipy.special.expit`` (v * sigmoid(v)); gelu against the
 exact erf GELU (``0.5 v (1 + erf(v / sqrt 2))``, ``math.erf``) within the tanh
 form's known approximation error, and its limits (0 at 0, v for large v, 0 for
-very negative v); the pair against a brute-force loop (``tests/test_oracle.py``).
+very negative v); the pair against a brute-force loop; ``glu_error_bound`` by
+perturbing both products within their bounds and by planted errors beyond it
+(``tests/test_oracle.py``).
 """
 
 from __future__ import annotations
@@ -40,3 +42,20 @@ ACTS = {"silu": silu, "gelu": gelu_tanh}
 def glu(x: np.ndarray, gate_deq: np.ndarray, up_deq: np.ndarray, act: str) -> np.ndarray:
     """fp64 act(x @ G^T) * (x @ U^T) for x (M,K), G and U (N,K) dequantised weights."""
     return ACTS[act](ref_matmul(x, gate_deq)) * ref_matmul(x, up_deq)
+
+
+# |act'(v)| <= ACT_SLOPE for both activations (silu' lies in [-0.100, 1.100], the tanh
+# GELU's in [-0.129, 1.129])
+ACT_SLOPE = 1.13
+
+
+def glu_error_bound(x: np.ndarray, gate_deq: np.ndarray, up_deq: np.ndarray, act: str,
+                    ratio: float = 2e-3) -> np.ndarray:
+    """Per-element error bound (M,N) of act(g)*u given the north-star bound on each product,
+    |g_err| <= ratio*||x_m||*max|G_n| = Bg and likewise Bu: by the mean value theorem
+    |act(g+dg)(u+du) - act(g)u| <= ACT_SLOPE*|u|*Bg + |act(g)|*Bu + ACT_SLOPE*Bg*Bu."""
+    g, u = ref_matmul(x, gate_deq), ref_matmul(x, up_deq)
+    xn = np.linalg.norm(np.asarray(x, np.float64), axis=1)[:, None]
+    bg = ratio * xn * np.abs(np.asarray(gate_deq, np.float64)).max(axis=1)[None, :]
+    bu = ratio * xn * np.abs(np.asarray(up_deq, np.float64)).max(axis=1)[None, :]
+    return ACT_SLOPE * np.abs(u) * bg + np.abs(ACTS[act](g)) * bu + ACT_SLOPE * bg * bu

@@ -51,18 +51,19 @@ def run_case(dev, T, E, k, H, I, gs, seed, tokens=None, x_scale=1.0):
         return cache[("d", e)]
 
     idx, w = om.router_topk(logits[sel], k)
-    ref = np.zeros((len(sel), H))
-    for ti, t in enumerate(sel):
-        xt = x[t].astype(np.float64)
-        for s in range(k):
-            e = int(idx[ti, s])
-            a = gu_e(e).astype(np.float64) @ xt
-            h = om.silu(a[:I]) * a[I:]
-            ref[ti] += w[ti, s] * (dn_e(e).astype(np.float64) @ h)
-    err = y[sel] - ref
-    rel = np.linalg.norm(err) / np.linalg.norm(ref)
-    assert rel <= 1e-3, f"MoE T={T}: rel_fro={rel:.3e}"
+    ref, bound = om.routed_reference(x[sel], idx, w, gu_e, dn_e, I)
+    check_routed(y[sel], ref, bound, f"MoE T={T}")
     return y
+
+
+def check_routed(y, ref, bound, what):
+    """Both north-star bars on routed outputs: relative Frobenius error <= 1e-3 and,
+    per element, |err| <= 2e-3 * sum_s w_s * ||h_s|| * max|D_e row| (the dense bound
+    on each slot's down product, weighted like the output)."""
+    err = np.asarray(y, np.float64) - ref
+    rel = np.linalg.norm(err) / np.linalg.norm(ref)
+    worst = float(np.max(np.abs(err) / bound))
+    assert rel <= 1e-3 and worst <= 1.0, f"{what}: rel_fro={rel:.3e} max err/bound={worst:.3f}"
 
 
 @pytest.mark.parametrize("T", [1, 2, 4, 5, 40])
@@ -89,8 +90,9 @@ def test_moe_group_sizes(dev, gs):
 
 @pytest.mark.parametrize("T", [1, 16, 256])
 def test_moe_config5(dev, T):
-    # 128 experts, top-8, H=2048, I=768, gs=64; check up to 12 tokens against the oracle
-    tokens = None if T <= 16 else list(range(0, T, 23))
+    # 128 experts, top-8, H=2048, I=768, gs=64; at T = 256 every 4th token (64 tokens)
+    # against the oracle
+    tokens = None if T <= 16 else list(range(0, T, 4))
     run_case(dev, T, E=128, k=8, H=2048, I=768, gs=64, seed=100 + T, tokens=tokens)
 
 
@@ -146,16 +148,8 @@ def run_gguf_case(dev, T, E, k, H, I, seed, tokens=None, logits_dtype=torch.floa
                 cache[(kind, e)] = oq.dequant_q6_k(dn[e * H:(e + 1) * H], I)
         return cache[(kind, e)]
 
-    ref = np.zeros((len(sel), H))
-    for ti, t in enumerate(sel):
-        xt = x[t].astype(np.float64)
-        for s in range(k):
-            e = int(idx[ti, s])
-            a = deq("g", e).astype(np.float64) @ xt
-            h = om.silu(a[:I]) * a[I:]
-            ref[ti] += w[ti, s] * (deq("d", e).astype(np.float64) @ h)
-    rel = np.linalg.norm(y[sel] - ref) / np.linalg.norm(ref)
-    assert rel <= 1e-3, f"GGUF MoE T={T}: rel_fro={rel:.3e}"
+    ref, bound = om.routed_reference(x[sel], idx, w, lambda e: deq("g", e), lambda e: deq("d", e), I)
+    check_routed(y[sel], ref, bound, f"GGUF MoE T={T}")
     return y
 
 
@@ -167,8 +161,9 @@ def test_gguf_moe_small(dev, T):
 
 @pytest.mark.parametrize("T", [1, 16, 256])
 def test_gguf_moe_qwen3_shape(dev, T):
-    # Qwen3-MoE-like: 128 experts, top-8, H = 2048, I = 768; up to 12 tokens checked
-    tokens = None if T <= 16 else list(range(0, T, 23))
+    # Qwen3-MoE-like: 128 experts, top-8, H = 2048, I = 768; at T = 256 every 4th token
+    # (64 tokens) checked
+    tokens = None if T <= 16 else list(range(0, T, 4))
     run_gguf_case(dev, T, E=128, k=8, H=2048, I=768, seed=200 + T, tokens=tokens)
 
 

@@ -12,6 +12,7 @@ import pathlib
 import numpy as np
 import pytest
 
+from oracle import glu as og
 from oracle import moe as om
 from oracle import quant as oq
 
@@ -226,3 +227,67 @@ def test_glu_pair_brute_force():
                 fa = a / (1.0 + np.exp(-a)) if act == "silu" else \
                     0.5 * a * (1.0 + np.tanh(np.clip(0.7978845608028654 * (a + 0.044715 * a ** 3), -10, 10)))
                 assert abs(y[m, n] - fa * b) < 1e-12 * max(1.0, abs(fa * b))
+
+
+def test_glu_error_bound_pinned():
+    """glu_error_bound: products perturbed anywhere inside their per-element bounds keep
+    act(g)*u inside it (mean value theorem; random and corner perturbations), and a
+    planted output error of twice the bound is caught."""
+    rng = np.random.default_rng(3)
+    M, N, K = 3, 40, 64
+    x = rng.standard_normal((M, K))
+    G, U = rng.standard_normal((N, K)) * 0.3, rng.standard_normal((N, K)) * 0.3
+    for act in ("silu", "gelu"):
+        f = og.ACTS[act]
+        g, u = x @ G.T, x @ U.T
+        xn = np.linalg.norm(x, axis=1)[:, None]
+        bg = 2e-3 * xn * np.abs(G).max(axis=1)[None, :]
+        bu = 2e-3 * xn * np.abs(U).max(axis=1)[None, :]
+        bound = og.glu_error_bound(x, G, U, act)
+        for sg, su in [(1, 1), (1, -1), (-1, 1), (-1, -1)]:
+            err = f(g + sg * bg) * (u + su * bu) - f(g) * u
+            assert np.all(np.abs(err) <= bound * (1 + 1e-12))
+        for _ in range(20):
+            err = f(g + rng.uniform(-1, 1, g.shape) * bg) * (u + rng.uniform(-1, 1, u.shape) * bu) - f(g) * u
+            assert np.all(np.abs(err) <= bound * (1 + 1e-12))
+        planted = f(g) * u + 2 * bound * np.sign(rng.standard_normal(g.shape))
+        assert np.any(np.abs(planted - f(g) * u) > bound)
+    # the activations' slopes stay under ACT_SLOPE on a dense grid
+    v = np.linspace(-12, 12, 200001)
+    for act in ("silu", "gelu"):
+        slope = np.diff(og.ACTS[act](v)) / np.diff(v)
+        assert np.abs(slope).max() <= og.ACT_SLOPE
+
+
+def test_routed_reference_bound_pinned():
+    """routed_reference: a hand-computed one-token, two-slot case; outputs recomputed
+    with every gate, up and down product perturbed inside its dense bound stay inside
+    the bound (to first order: the perturbations are small); a planted error of twice
+    the bound is caught."""
+    I, H = 2, 3
+    Gs = {0: np.array([[1.0, 0, 0], [0, 1.0, 0], [1.0, 1.0, 0], [0, 0, 2.0]]),   # (2I, H): gate rows, up rows
+          1: np.array([[0, 0, 1.0], [1.0, 0, 0], [0, 2.0, 0], [1.0, 0, 1.0]])}
+    Ds = {0: np.array([[1.0, 2.0], [0, -3.0], [0.5, 0]]), 1: np.array([[-1.0, 0], [2.0, 2.0], [0, 4.0]])}
+    x = np.array([[1.0, 2.0, 3.0]])
+    idx = np.array([[1, 0]])
+    w = np.array([[0.75, 0.25]])
+    ref, bound = om.routed_reference(x, idx, w, lambda e: Gs[e], lambda e: Ds[e], I)
+    want_ref = np.zeros(H)
+    for s, e in enumerate((1, 0)):
+        a = Gs[e] @ x[0]
+        h = np.array([a[j] / (1 + np.exp(-a[j])) * a[I + j] for j in range(I)])
+        want_ref += w[0, s] * (Ds[e] @ h)
+    assert np.allclose(ref[0], want_ref, rtol=1e-14)
+    # random perturbations of every product inside its bound
+    rng = np.random.default_rng(8)
+    xn = np.linalg.norm(x[0])
+    for _ in range(200):
+        y = np.zeros(H)
+        for s, e in enumerate((1, 0)):
+            a = Gs[e] @ x[0] + rng.uniform(-1, 1, 2 * I) * 2e-3 * xn * np.abs(Gs[e]).max(axis=1)
+            h = om.silu(a[:I]) * a[I:]
+            d = Ds[e] @ h + rng.uniform(-1, 1, H) * 2e-3 * np.linalg.norm(h) * np.abs(Ds[e]).max(axis=1)
+            y += w[0, s] * d
+        assert np.all(np.abs(y - ref[0]) <= bound[0] * (1 + 1e-9))
+    planted = ref[0] + 2 * bound[0]
+    assert np.all(np.abs(planted - ref[0]) > bound[0])
