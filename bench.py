@@ -14,12 +14,14 @@ Prints ONE JSON line.  The step's 197 launches are captured once in a HIP graph 
 launch-bound otherwise); ``value`` = total weight bytes x K / elapsed time of K
 graph replays (HIP events on the replay stream, synchronized on both sides).
 ``roofline`` is for the dominant kernel (the Q4_K v_dot2 GEMV): its average
-launch duration per weight shape comes from a graph of all 28 launches of that
-shape (each layer's own weights, so HBM-cold), timed the same way.  ``cpu_baseline``
-times the CPU oracle (NumPy dequant + PyTorch-CPU fp32 matmul) on one layer.
-``prefill_gemm`` reports the Q4_K MFMA GEMM at M = 512, 2048, 4096 on the three config-4 shapes;
+launch duration per weight shape comes from a graph of launches over distinct weights
+of that shape totalling >= 512 MB (HBM-cold), timed the same way (``--roofline-only``
+runs just these graphs, for the profiler).  ``cpu_baseline`` times the CPU restatement
+(NumPy dequant + PyTorch-CPU fp32 matmul) on one layer and on configs 1, 3, 4 and 5.
+``prefill_gemm`` reports the Q4_K MFMA GEMM at M = 512, 2048, 4096 on the three config-4
+shapes, ``prefill_gemm_other_formats`` the other formats' GEMM at M = 2048;
 ``other_configs`` the remaining BASELINE configurations (1, 3 and 5) with their weight
-GB/s, each timed over rotating weight copies larger than the Infinity Cache.
+GB/s, each timed over rotating weight copies of >= 512 MB.
 """
 
 from __future__ import annotations
@@ -124,9 +126,13 @@ def time_replays(g, steps, warmup, stream):
     return start.elapsed_time(end) / 1000.0
 
 
+MIN_ROTATE_BYTES = 512_000_000   # 2x the 256 MB Infinity Cache: every launch reads its weights from HBM
+
+
 def per_shape_times(mats, xs, ys, qmm, dev, reps=5):
-    """Average launch duration per weight shape: a graph of all launches of that shape
-    (every layer's own weights, so HBM-cold), replayed `reps` times, divided by launches."""
+    """Average launch duration per weight shape: a graph of launches over distinct
+    weights totalling >= 512 MB (the step's own matrices of that shape, plus copies),
+    replayed `reps` times, divided by launches (HBM-cold, inter-kernel gaps included)."""
     import torch
 
     from alloy_amd import synth
@@ -134,47 +140,123 @@ def per_shape_times(mats, xs, ys, qmm, dev, reps=5):
     stream = torch.cuda.current_stream(dev)
     out = {}
     for key in sorted({(K, N) for _, K, N, _ in mats}):
+        K, N = key
         sel = [m for m in mats if (m[1], m[2]) == key]
-        if len(sel) == 1:                       # lm_head: 3 copies (663 MB) rotate past the MALL
-            K, N = key
-            sel = sel + [(f"copy{i}", K, N, synth.torch_blocks("q4_k", N, K, 4242 + i, dev)) for i in range(2)]
-        seq = sel * max(1, 28 // len(sel))
+        need = max(len(sel), -(-MIN_ROTATE_BYTES // q4k_bytes(K, N)))
+        seq = sel + [(f"copy{i}", K, N, synth.torch_blocks("q4_k", N, K, 4242 + i, dev))
+                     for i in range(need - len(sel))]
         g = capture(lambda: [qmm("q4_k", xs[K], w, out=ys[N]) for _, K, N, w in seq], dev)
         t = time_replays(g, reps, 2, stream)
         out[key] = t / (reps * len(seq))
-        del g
+        del g, seq
     return out
 
 
-def cpu_baseline(seconds_target=15.0):
-    """CPU oracle on one transformer layer's 7 matrices: NumPy dequant + torch fp32 matmul."""
+def _median_time(fn, budget_s, max_reps=20, min_reps=3):
+    fn()                                              # warm-up
+    times, t_all = [], time.perf_counter()
+    while len(times) < min_reps or (time.perf_counter() - t_all < budget_s and len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2], len(times)
+
+
+def roofline(mats, xs, ys, qmm, dev, total_bytes):
+    """Roofline of the dominant kernel (the Q4_K M=1 GEMV): each weight shape's average
+    launch duration (per_shape_times), weighted by its launches in the step; algorithmic
+    bytes of a launch = its N*K/256*144 weight bytes."""
+    per = per_shape_times(mats, xs, ys, qmm, dev)
+    counts = {}
+    for _, K, N, _ in mats:
+        counts[(K, N)] = counts.get((K, N), 0) + 1
+    tot_t = sum(per[k] * c for k, c in counts.items())
+    achieved = total_bytes / tot_t / 1e9
+    launches = len(mats)
+    shapes = {f"{K}x{N}": {"us": round(v * 1e6, 2), "GBps": round(q4k_bytes(K, N) / v / 1e9, 1),
+                           "launches_per_step": counts[(K, N)]}
+              for (K, N), v in per.items()}
+    return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
+            "kernel": "k_gemv_w<FQ4K> (Q4_K M=1 wave-row GEMV)",
+            "bytes_per_launch": round(total_bytes / launches),
+            "avg_launch_us": round(tot_t / launches * 1e6, 3), "per_shape": shapes}
+
+
+def cpu_baseline():
+    """The reference path's CPU restatement, timed on this host: NumPy decode of the wire
+    blocks (the oracle's formulas) + PyTorch-CPU fp32 matmul, per call, and the matmul
+    alone on pre-decoded weights.  Headline row: one Llama-3.2-3B layer (config 2, M=1);
+    further rows: config 1, config 3 (one Q6_K and one Q5_0 shape, M=1), config 4
+    (M=512, one shape), config 5 (MLX MoE, T=1)."""
     import numpy as np
     import torch
 
     from alloy_amd import synth
+    from oracle import moe as om
     from oracle import quant as oq
 
     torch.set_num_threads(os.cpu_count() or 1)
     rng = np.random.default_rng(0)
+    rows = []
+
+    def dense_row(name, fmt, K, N, M, budget):
+        blob = synth.numpy_blocks(fmt, N, K, rng)
+        x = torch.from_numpy(synth.numpy_x(M, K, rng)).float()
+        W = torch.from_numpy(oq.dequant(fmt, blob, K))
+        t_full, n_full = _median_time(lambda: torch.matmul(x, torch.from_numpy(oq.dequant(fmt, blob, K)).T), budget)
+        t_mm, n_mm = _median_time(lambda: torch.matmul(x, W.T), budget / 4)
+        nbytes = blob.nbytes
+        rows.append({"config": name, "format": fmt, "M": M, "K": K, "N": N, "weight_bytes": nbytes,
+                     "dequant_matmul_ms": round(t_full * 1e3, 3), "matmul_only_ms": round(t_mm * 1e3, 3),
+                     "weight_GBps": round(nbytes / t_full / 1e9, 4), "TFLOPs": round(2 * M * N * K / t_full / 1e12, 5),
+                     "reps": [n_full, n_mm]})
+
+    # headline: config 2, one transformer layer (7 matrices), M = 1
     layer = [(K, N, synth.numpy_blocks("q4_k", N, K, rng)) for _, K, N in LLAMA32_3B]
     xs = {K: torch.from_numpy(synth.numpy_x(1, K, rng)).float() for K in (3072, 8192)}
+    Ws = [torch.from_numpy(oq.dequant_q4_k(b, K)) for K, _, b in layer]
     nbytes = sum(q4k_bytes(K, N) for K, N, _ in layer)
+    t_layer, n_layer = _median_time(lambda: [torch.matmul(xs[K], torch.from_numpy(oq.dequant_q4_k(b, K)).T)
+                                             for K, _, b in layer], 5.0)
+    t_layer_mm, _ = _median_time(lambda: [torch.matmul(xs[K], W.T) for (K, _, _), W in zip(layer, Ws)], 1.5)
+    del Ws
+    rows.append({"config": "config2 Llama-3.2-3B layer (7 matrices)", "format": "q4_k", "M": 1, "weight_bytes": nbytes,
+                 "dequant_matmul_ms": round(t_layer * 1e3, 3), "matmul_only_ms": round(t_layer_mm * 1e3, 3),
+                 "weight_GBps": round(nbytes / t_layer / 1e9, 4), "reps": [n_layer]})
+    dense_row("config1", "q8_0", 4096, 4096, 1, 2.0)
+    dense_row("config3", "q6_k", 4096, 4096, 1, 2.0)
+    dense_row("config3", "q5_0", 4096, 4096, 1, 2.0)
+    dense_row("config4", "q4_k", 4096, 4096, 512, 3.0)
+    # config 5: MLX MoE, T = 1 (router + the 8 routed experts' gate/up and down)
+    E, k, H, I, gs = 128, 8, 2048, 768, 64
+    gu = [synth.numpy_mlx(2 * I, H, gs, rng) for _ in range(E)]
+    dn = [synth.numpy_mlx(H, I, gs, rng) for _ in range(E)]
+    x5 = synth.numpy_x(1, H, rng).astype(np.float32)
+    lg = rng.standard_normal((1, E)).astype(np.float32)
 
-    def one():
-        for K, N, blob in layer:
-            W = torch.from_numpy(oq.dequant_q4_k(blob, K))
-            torch.matmul(xs[K], W.T)
+    def moe(decoded=None):
+        idx, w = om.router_topk(lg, k)
+        y = torch.zeros(H)
+        xt = torch.from_numpy(x5[0])
+        for s_ in range(k):
+            e = int(idx[0, s_])
+            G, D = decoded[e] if decoded else (torch.from_numpy(oq.dequant_mlx_q4(*gu[e], gs)),
+                                               torch.from_numpy(oq.dequant_mlx_q4(*dn[e], gs)))
+            a = G @ xt
+            h = torch.nn.functional.silu(a[:I]) * a[I:]
+            y += float(w[0, s_]) * (D @ h)
+        return y
 
-    one()   # warm-up
-    times = []
-    t_all = time.perf_counter()
-    while time.perf_counter() - t_all < seconds_target or len(times) < 3:
-        t0 = time.perf_counter()
-        one()
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 50:
-            break
-    med = sorted(times)[len(times) // 2]
+    t_moe, n_moe = _median_time(moe, 2.0)
+    used = {int(e) for e in om.router_topk(lg, k)[0][0]}
+    dec = {e: (torch.from_numpy(oq.dequant_mlx_q4(*gu[e], gs)), torch.from_numpy(oq.dequant_mlx_q4(*dn[e], gs)))
+           for e in used}
+    t_moe_mm, _ = _median_time(lambda: moe(dec), 0.5)
+    moe_bytes = len(used) * (2 * I * (H // 2 + 4 * H // gs) + H * (I // 2 + 4 * I // gs))
+    rows.append({"config": "config5 MLX MoE", "format": "mlx_q4", "T": 1, "weight_bytes": moe_bytes,
+                 "dequant_matmul_ms": round(t_moe * 1e3, 3), "matmul_only_ms": round(t_moe_mm * 1e3, 3),
+                 "weight_GBps": round(moe_bytes / t_moe / 1e9, 4), "reps": [n_moe]})
     model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -184,15 +266,18 @@ def cpu_baseline(seconds_target=15.0):
     except OSError:
         pass
     return {
-        "value": round(nbytes / med / 1e9, 4),
+        "value": rows[0]["weight_GBps"],
         "unit": "weight GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"one Llama-3.2-3B layer (7 Q4_K matrices, {nbytes} weight bytes), M=1, "
-                  f"NumPy dequant + torch fp32 matmul per call, median of {len(times)} reps",
-        "ms_per_call": round(med * 1e3, 2),
+        "sample": f"one Llama-3.2-3B layer (7 Q4_K matrices, {nbytes} weight bytes), M=1, NumPy dequant + torch "
+                  f"fp32 matmul per call, median of {n_layer} reps; further rows: configs 1, 3 (4096x4096), 4 (M=512, 4096x4096), "
+                  f"5 (T=1), each also timed as matmul only on pre-decoded weights",
+        "ms_per_call": rows[0]["dequant_matmul_ms"],
         "cpu_model": model,
         "os_cpu_count": os.cpu_count(),
+        "torch_threads": torch.get_num_threads(),
+        "rows": rows,
     }
 
 
@@ -227,6 +312,34 @@ def prefill_gemm(dev, qmm, Ms=(512, 2048, 4096), reps=10, opts=0, eager=False):
         out.append({"M": M, "K": K, "N": N, "us": round(t * 1e6, 1), "tflops": round(tf, 2),
                     "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)})
         del w, x, y
+    return out
+
+
+def prefill_gemm_other_formats(dev, qmm, M=2048, reps=5):
+    """The prefill GEMM of the other formats (generic double-buffered kernel) on config-4
+    shapes at M = 2048, graph replays, fp32 output."""
+    import torch
+
+    from alloy_amd import synth
+
+    out = []
+    for fmt in ("q8_0", "q5_0", "q6_k", "mlx_q4"):
+        for K, N in [(4096, 4096), (4096, 14336)]:
+            if fmt == "mlx_q4":
+                q, sc, bi = synth.torch_mlx(N, K, 64, 90 + N, dev)
+                fn_w = lambda xx, yy: qmm("mlx_q4", xx, q, scales=sc, biases=bi, group_size=64, out=yy,  # noqa: E731
+                                          path="gemm")
+            else:
+                w = synth.torch_blocks(fmt, N, K, 90 + N, dev)
+                fn_w = lambda xx, yy, w=w, fmt=fmt: qmm(fmt, xx, w, out=yy, path="gemm")  # noqa: E731
+            x = synth.torch_x(M, K, 91 + K, dev)
+            y = torch.empty((M, N), dtype=torch.float32, device=dev)
+            g = capture(lambda: fn_w(x, y), dev)
+            t = time_replays(g, reps, 2, torch.cuda.current_stream(dev)) / reps
+            tf = 2.0 * M * N * K / t / 1e12
+            out.append({"format": fmt, "M": M, "K": K, "N": N, "us": round(t * 1e6, 1), "tflops": round(tf, 2),
+                        "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)})
+            del g, x, y
     return out
 
 
@@ -269,7 +382,7 @@ def other_configs(dev, qmm, eager=False):
 
     def gemv_case(fmt, K, N, M, seed):
         nbytes = formats.row_bytes(fmt, K) * N
-        ncopy = max(2, -(-320_000_000 // nbytes))
+        ncopy = max(2, -(-MIN_ROTATE_BYTES // nbytes))
         ws = [synth.torch_blocks(fmt, N, K, seed + i, dev) for i in range(ncopy)]
         x = synth.torch_x(M, K, seed, dev)
         y = torch.empty((M, N), dtype=torch.float32, device=dev)
@@ -289,16 +402,11 @@ def other_configs(dev, qmm, eager=False):
     # config 5: MLX MoE
     E, k, H, I, gs = 128, 8, 2048, 768, 64
     experts = []
-    for c in range(3):
-        g = torch.Generator(device=dev)
-        g.manual_seed(500 + c)
-        experts.append((
-            torch.randint(0, 256, (E, 2 * I, H // 2), dtype=torch.uint8, device=dev, generator=g),
-            (torch.rand((E, 2 * I, H // gs), device=dev, generator=g) * 0.01).half(),
-            ((torch.rand((E, 2 * I, H // gs), device=dev, generator=g) - 0.5) * 0.02).half(),
-            torch.randint(0, 256, (E, H, I // 2), dtype=torch.uint8, device=dev, generator=g),
-            (torch.rand((E, H, I // gs), device=dev, generator=g) * 0.01).half(),
-            ((torch.rand((E, H, I // gs), device=dev, generator=g) - 0.5) * 0.02).half()))
+    for c in range(2):                       # 2 x 340 MB rotate past the Infinity Cache
+        gq, gsc, gbi = synth.torch_mlx(E * 2 * I, H, gs, 500 + c, dev)   # scales |N(0,1)|*0.01, biases N(0, 0.01)
+        dq, dsc, dbi = synth.torch_mlx(E * H, I, gs, 600 + c, dev)
+        experts.append((gq.view(E, 2 * I, H // 2), gsc.view(E, 2 * I, H // gs), gbi.view(E, 2 * I, H // gs),
+                        dq.view(E, H, I // 2), dsc.view(E, H, I // gs), dbi.view(E, H, I // gs)))
     per_expert = sum(t.numel() * t.element_size() for t in experts[0]) // E
     moe = {}
     for T in (1, 16, 256):
@@ -353,6 +461,10 @@ def main():
                     help="time the decode step only (no per-shape, prefill or CPU legs)")
     ap.add_argument("--eager", action="store_true",
                     help="launch eagerly instead of replaying HIP graphs (counter runs; decode step or configs)")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="time only the per-shape graphs the roofline is computed from (profiler runs)")
+    ap.add_argument("--cpu-only", action="store_true",
+                    help="run only the CPU baseline (no GPU needed) and print it")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 256 MiB device copy (counter calibration) and exit")
     ap.add_argument("--configs-only", action="store_true",
@@ -367,6 +479,9 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    if args.cpu_only:
+        print(json.dumps({"cpu_baseline": cpu_baseline()}))
+        return
     import torch
 
     import alloy_amd
@@ -387,6 +502,9 @@ def main():
     log("building decode step weights ...")
     mats, xs, ys = build_decode_step(dev)
     total_bytes = sum(q4k_bytes(K, N) for _, K, N, _ in mats)
+    if args.roofline_only:
+        print(json.dumps({"roofline": roofline(mats, xs, ys, qmm, dev, total_bytes)}))
+        return
     stream = torch.cuda.current_stream(dev)
     if args.eager:
         log(f"{len(mats)} GEMVs, {total_bytes} weight bytes; eager launches")
@@ -420,20 +538,15 @@ def main():
                        "(one launch serving several matrices), fp16 outputs"}
     log(json.dumps({"batched_step": batched}))
 
-    per = per_shape_times(mats, xs, ys, qmm, dev)
-    counts = {}
-    for _, K, N, _ in mats:
-        counts[(K, N)] = counts.get((K, N), 0) + 1
-    tot_t = sum(per[k] * c for k, c in counts.items())
-    achieved = total_bytes / tot_t / 1e9
-    launches = len(mats)
-    shapes = {f"{K}x{N}": {"us": round(v * 1e6, 2), "GBps": round(q4k_bytes(K, N) / v / 1e9, 1)}
-              for (K, N), v in per.items()}
-    log(json.dumps(shapes))
+    roof = roofline(mats, xs, ys, qmm, dev, total_bytes)
+    log(json.dumps(roof["per_shape"]))
 
     prefill = None if args.no_prefill else prefill_gemm(dev, qmm)
     if prefill:
         log(json.dumps(prefill))
+    prefill_other = None if args.no_prefill else prefill_gemm_other_formats(dev, qmm)
+    if prefill_other:
+        log(json.dumps({"prefill_gemm_other_formats": prefill_other}))
     cpu = None if args.no_cpu else cpu_baseline()
     configs = None if args.no_configs else other_configs(dev, qmm)
     if configs:
@@ -455,13 +568,10 @@ def main():
         "config": {"workload": "Llama-3.2-3B Q4_K decode step, M=1: 28 layers x (q,k,v,o,gate,up,down) + lm_head",
                    "launches_per_step": launches, "weight_bytes_per_step": total_bytes,
                    "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
-                     "kernel": "k_gemv_w<FQ4K> (Q4_K M=1 wave-row GEMV)",
-                     "bytes_per_launch": round(total_bytes / launches),
-                     "avg_launch_us": round(tot_t / launches * 1e6, 3), "per_shape": shapes},
+        "roofline": roof,
         "cpu_baseline": cpu,
         "prefill_gemm": prefill,
+        "prefill_gemm_other_formats": prefill_other,
         "batched_step": batched,
         "other_configs": configs,
     }
