@@ -112,14 +112,21 @@ struct Src {
     b = __builtin_amdgcn_make_buffer_rsrc((void*)a.b, (short)0, a.b ? (int)sbytes : 0, ALLOY_RSRC_DW3);
   }
 };
+// P: cache-policy bits of the load (gfx950: 1 sc0, 2 nt, 16 sc1).  kStream marks a
+// load whose bytes no other wave reads again (weights streamed once by the M = 1
+// GEMV): non-temporal, so they do not push the shared x vector out of the caches.
+constexpr int kStream = 2;
+template <int P = 0>
 __device__ __forceinline__ u32x4 bld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, P);
 }
+template <int P = 0>
 __device__ __forceinline__ uint32_t bld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, P);
 }
+template <int P = 0>
 __device__ __forceinline__ uint32_t bld2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, P);
 }
 // NW little-endian words at a 2-byte-aligned offset: aligned dword loads plus one
 // u16 load, merged with v_alignbyte (same bytes as ld_words_a2).
@@ -232,8 +239,8 @@ struct FQ4K {
   // bytes through the address unit instead of the whole header per lane.
   __device__ static Raw load_b(const Src& src, uint32_t wo, uint32_t, int u) {
     Raw r;
-    r.h = u32x4{bld4(src.w, wo + 4u * (uint32_t)(u & 3)), 0u, 0u, 0u};
-    r.q = bld16(src.w, wo + 16 + 16 * (u & 7));
+    r.h = u32x4{bld4<kStream>(src.w, wo + 4u * (uint32_t)(u & 3)), 0u, 0u, 0u};
+    r.q = bld16<kStream>(src.w, wo + 16 + 16 * (u & 7));
     return r;
   }
   __device__ static void share(Raw& r) {
