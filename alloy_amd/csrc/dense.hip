@@ -2,6 +2,9 @@
 // M=1 GEMV (v_dot2), M<=16 GEMV on MFMA and the gated pair (the prefill GEMM is in
 // gemm.hip).  All launched on the caller's
 // HIP stream; no allocation, no global mutable state.
+#include <map>
+#include <mutex>
+#include <tuple>
 #include <type_traits>
 
 #include "gemv.h"
@@ -585,6 +588,37 @@ __global__ __launch_bounds__((m4_max_threads<TG, SPW>())) void k_gemv_q4k_m4(QAr
 }
 
 // ------------------------------------------------------------------ host launchers
+
+namespace {
+std::mutex g_occ_mu;
+std::map<std::tuple<int, const void*, int, size_t>, int> g_occ;   // (device, kernel, threads, lds)
+std::map<int, int> g_cus;                                           // device -> compute units
+}  // namespace
+
+int cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> g(g_occ_mu);
+  auto it = g_cus.find(dev);
+  if (it != g_cus.end()) return it->second;
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+  g_cus[dev] = v;
+  return v;
+}
+
+int resident_per_cu(const void* kern, int threads, size_t lds) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 1;
+  const auto key = std::make_tuple(dev, kern, threads, lds);
+  std::lock_guard<std::mutex> g(g_occ_mu);
+  auto it = g_occ.find(key);
+  if (it != g_occ.end()) return it->second;
+  int v = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, kern, threads, lds) != hipSuccess || v <= 0) v = 1;
+  g_occ[key] = v;
+  return v;
+}
 template <template <class> class Fn, typename... Args>
 static hipError_t by_fmt(int fmt, Args&&... args) {
   switch (fmt) {
@@ -791,7 +825,7 @@ struct GemvWaveRun {
     // up to three workgroups per CU (two at four units per lane, where the register
     // budget leaves three resident), looping when the rows need more; very tall
     // matrices (lm_head) with eight per CU — measured on the decode shapes
-    const int cus = xs_cu_count();
+    const int cus = cu_count();
     const int cap = o.grid_cap > 0 ? o.grid_cap : (N > 32768 ? 8 * cus : upt >= 4 ? 2 * cus : 3 * cus);
     return y_f32 ? pick<float>(upt, depth, b, sb, x, M, lshift, cap, st)
                  : pick<f16>(upt, depth, b, sb, x, M, lshift, cap, st);
@@ -1097,7 +1131,7 @@ static hipError_t launch_gemv_xs(int fmt, const QArgs& a, const void* x, bool x_
     // measured on the config 2 / 3 shapes: wide matrices loop one workgroup per CU
     // over their tiles (next tiles' weights in flight); Q4_K at M > 8 on mid-size N
     // takes two tiles per reduction
-    const int64_t dcap = o.grid_cap > 0 ? o.grid_cap : N >= 12288 ? xs_cu_count() : 1024;
+    const int64_t dcap = o.grid_cap > 0 ? o.grid_cap : N >= 12288 ? cu_count() : 1024;
     const int rt = o.row_groups ? o.row_groups : fmt == F_Q4_K && M > 8 && N > 4096 && N < 12288 ? 2 : 1;
     if (fmt == F_Q4_K) return launch_xs<XsDQ<XsQ4K>, 0>(j, 0, dcap, rt, st);
     if (fmt == F_Q6_K) return launch_xs<XsDQ<XsQ6K>, 0>(j, 0, dcap, rt, st);

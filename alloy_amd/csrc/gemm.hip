@@ -396,7 +396,7 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float* ws, int S, int6
 // HBM traffic) and one launch.  S divides the super-blocks, at least two per split.
 struct GemmPlan { int kind, splits; };
 static GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K, bool allow_split) {
-  const int cus = xs_cu_count();
+  const int cus = cu_count();
   const int bm[5] = {256, 128, 128, 64, 64}, bn[5] = {256, 256, 128, 256, 128};
   const double rate[5] = {1000e12, 790e12, 600e12, 590e12, 420e12};
   const double flops = 2.0 * (double)M * (double)N * (double)K;

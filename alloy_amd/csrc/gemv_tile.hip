@@ -15,7 +15,6 @@
 // and token.
 // The grid is persistent (resident workgroups); workgroup bx walks tiles bx, bx +
 // grid, ...; rows past N read as zeros (buffer loads past the end) and are not stored.
-#include <atomic>
 
 #include "gemv.h"
 #include "launch.h"
@@ -127,17 +126,6 @@ __global__ __launch_bounds__(256) void k_gemv_t(QArgs a, const f16* x, int M, YT
 
 namespace {
 
-template <class Kern>
-int tile_resident_per_cu(Kern kern, size_t lds) {
-  static std::atomic<int> cached[64];
-  const int key = (int)(lds >> 12) < 63 ? (int)(lds >> 12) : 63;
-  int v = cached[key].load(std::memory_order_relaxed);
-  if (v > 0) return v;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, kern, 256, lds) != hipSuccess || v <= 0) v = 1;
-  cached[key].store(v, std::memory_order_relaxed);
-  return v;
-}
-
 template <class F>
 hipError_t run_tile(const QArgs& a, const void* x, void* y, bool y_f32, int64_t M, int64_t N64, const Opts& o,
                     hipStream_t st) {
@@ -152,8 +140,8 @@ hipError_t run_tile(const QArgs& a, const void* x, void* y, bool y_f32, int64_t 
   if (cpl > kMaxCpl || lds > 160 * 1024) return hipErrorNotSupported;
   const int N = (int)N64;
   const int ntiles = (N + kTileRows - 1) / kTileRows;
-  int grid = (y_f32 ? tile_resident_per_cu(k_gemv_t<F, float>, lds) : tile_resident_per_cu(k_gemv_t<F, f16>, lds)) *
-             xs_cu_count();
+  int grid = resident_per_cu(y_f32 ? (const void*)k_gemv_t<F, float> : (const void*)k_gemv_t<F, f16>, 256, lds) *
+             cu_count();
   if (o.grid_cap > 0 && o.grid_cap < grid) grid = o.grid_cap;
   if (grid > ntiles) grid = ntiles;
   if (y_f32)

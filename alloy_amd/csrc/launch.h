@@ -73,6 +73,12 @@ hipError_t launch_glu_fused(int fmt, int act, const QArgs& g, const QArgs& u, co
 hipError_t launch_glu_combine(int act, const float* g, const float* u, void* y, bool y_f32, int64_t n,
                               hipStream_t st);
 
+// Compute units of the current device, and the workgroups of `kern` (`threads` per
+// workgroup, `lds` bytes of dynamic LDS) resident per compute unit on it: both
+// queried once per (device, kernel, launch shape) and kept for the process.
+int cu_count();
+int resident_per_cu(const void* kern, int threads, size_t lds);
+
 // The v_dot2 GEMV gives each thread at most 2 decode units of a 256-thread row:
 // K <= 512 units per row.
 inline int64_t max_k_dot2(int fmt) { return fmt == F_Q6_K ? 512 * 64 : 512 * 32; }

@@ -727,7 +727,7 @@ static hipError_t launch_routed(const QArgs& a, uint32_t sb, int32_t* idx, float
   const int U = a.K / F::UE;
   if (a.K % 256 || U > 256 || (MODE == 1 && a.K > 4096)) return hipErrorNotSupported;
   int lshift = U <= 64 ? 4 : U <= 128 ? 5 : 6;
-  const int cus = xs_cu_count();
+  const int cus = cu_count();
   while (lshift < 6 && R * ((int64_t)N << lshift) < (int64_t)2 * cus * 256) ++lshift;   // enough workgroups
   const int L = 1 << lshift, upt = (U + L - 1) / L, rows = 256 >> lshift;
   if (upt > 4) return hipErrorNotSupported;

@@ -15,7 +15,6 @@
 //
 // Units: 256 elements of a row; a wave owns NS/8 units (8 activation slots each).
 #pragma once
-#include <atomic>
 #include <type_traits>
 #include "gemv.h"
 #include "launch.h"
@@ -717,30 +716,6 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
   run(std::integral_constant<int, TT>());
 }
 
-// Compute units of the current device (cached per device).
-inline int xs_cu_count() {
-  static std::atomic<int> cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  int v = cached[dev].load(std::memory_order_relaxed);
-  if (v > 0) return v;
-  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-  cached[dev].store(v, std::memory_order_relaxed);
-  return v;
-}
-
-// Workgroups of `kern` with W waves (and the LDS that W implies) resident per CU
-// (cached per kernel and W).
-template <class Kern>
-int xs_resident_per_cu(Kern kern, int W, size_t lds) {
-  static std::atomic<int> cached[17];
-  int v = cached[W].load(std::memory_order_relaxed);
-  if (v > 0) return v;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, kern, 64 * W, lds) != hipSuccess || v <= 0) v = 1;
-  cached[W].store(v, std::memory_order_relaxed);
-  return v;
-}
-
 // Host launcher.  hipErrorNotSupported when the shape does not fit the kernel
 // (K not a multiple of 256 or over 8192, offsets of 2 GiB or more): the caller then
 // uses another kernel.  MODE 0: one 16-row tile (rt = 1) or two (rt = 2) per
@@ -780,7 +755,7 @@ hipError_t launch_xs(const XsJob& j, int64_t tiles_y, int64_t cap, int rt, hipSt
     }
     int64_t gx = groups;
     if (pipe) {
-      const int64_t c = cap > 0 ? cap : (int64_t)xs_resident_per_cu(kern, W, lds) * xs_cu_count();
+      const int64_t c = cap > 0 ? cap : (int64_t)resident_per_cu((const void*)kern, 64 * W, lds) * cu_count();
       gx = groups < c ? groups : c;
     }
     const dim3 grid((unsigned)gx, DENSE ? 1u : (unsigned)tiles_y), block((unsigned)(64 * W));
@@ -791,7 +766,7 @@ hipError_t launch_xs(const XsJob& j, int64_t tiles_y, int64_t cap, int rt, hipSt
   };
   // whether the tiles outnumber the resident workgroups of the one-pass kernel
   auto many = [&](auto kern) -> bool {
-    const int64_t c = cap > 0 ? cap : (int64_t)xs_resident_per_cu(kern, W, lds) * xs_cu_count();
+    const int64_t c = cap > 0 ? cap : (int64_t)resident_per_cu((const void*)kern, 64 * W, lds) * cu_count();
     return groups > c;
   };
   using I1 = std::integral_constant<int, 1>;

@@ -10,8 +10,9 @@
  * Conventions
  *   - Every pointer is a DEVICE pointer owned by the caller; the library never
  *     allocates device memory.  Its only state is a per-process cache of device
- *     attributes (CU count per device, kernel occupancy per kernel), filled on first
- *     use under atomics; results never depend on earlier calls.
+ *     attributes (CU count per device; resident workgroups per device, kernel and
+ *     launch shape), filled on first use under a mutex, and the static scratch
+ *     array of alloy_gguf_moe_routed_noalloc; results never depend on earlier calls.
  *   - `stream` is a hipStream_t (NULL = default stream); all work is enqueued on
  *     it, asynchronously.  Calls are reentrant; concurrent calls on different
  *     streams do not interact.
