@@ -1112,7 +1112,8 @@ struct GemvMfmaRun {
 };
 
 // M <= 16 on the generic x-stationary kernel (Q4_K, Q6_K, MLX with a power-of-two
-// group size); hipErrorNotSupported when the format or shape does not fit it.
+// group size; GGUF wire Q5_0 / Q8_0 with dequantised weights only); hipErrorNotSupported
+// when the format or shape does not fit it.
 static hipError_t launch_gemv_xs(int fmt, const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32,
                                  int64_t M, int64_t N, const Opts& o, hipStream_t st, bool dq = false) {
   if (x_f32 || M > 16 || N >= (1ll << 31) || (uint64_t)M * (uint64_t)a.K * 2u >= (1ull << 31))
@@ -1135,6 +1136,8 @@ static hipError_t launch_gemv_xs(int fmt, const QArgs& a, const void* x, bool x_
     const int rt = o.row_groups ? o.row_groups : fmt == F_Q4_K && M > 8 && N > 4096 && N < 12288 ? 2 : 1;
     if (fmt == F_Q4_K) return launch_xs<XsDQ<XsQ4K>, 0>(j, 0, dcap, rt, st);
     if (fmt == F_Q6_K) return launch_xs<XsDQ<XsQ6K>, 0>(j, 0, dcap, rt, st);
+    if (fmt == F_Q5_0) return launch_xs<XsDQ<XsQ50>, 0>(j, 0, dcap, rt, st);
+    if (fmt == F_Q8_0) return launch_xs<XsDQ<XsQ80>, 0>(j, 0, dcap, rt, st);
   } else {
     if (fmt == F_Q4_K) return launch_xs<XsQ4K, 0>(j, 0, cap, o.row_groups, st);
     if (fmt == F_Q6_K) return launch_xs<XsQ6K, 0>(j, 0, cap, o.row_groups, st);
@@ -1204,11 +1207,12 @@ hipError_t launch_glu_combine(int act, const float* g, const float* u, void* y, 
   return hipGetLastError();
 }
 
-// Default kernel choice for 2 <= M <= 16 (measured on the config 2 / 3 shapes):
+// Default kernel choice for 2 <= M <= 16 (measured on the config 1 / 2 / 3 shapes):
 //   Q4_K  tall (N >= 32768) and 3 <= M <= 6: 4x4x4 broadcast kernel; K <= 8192: the
 //         x-stationary kernel with fp16-dequantised weights (8); else the Q4_K
 //         x-stationary kernel
-//   Q6_K  K <= 4096: x-stationary with fp16-dequantised weights, else 16x16x32
+//   Q6_K, Q5_0, Q8_0 (wire blocks)  x-stationary with fp16-dequantised weights (K over
+//         4096: in passes over K)
 //   MLX   generic x-stationary (exact products); N >= 12288: the dequantising
 //         provider with 16-byte loads, one workgroup per CU looping over the tiles
 //   other formats (and shapes the above do not take): 16x16x32 kernel
@@ -1217,7 +1221,7 @@ static int mfma_variant(int fmt, int64_t M, int64_t N, int64_t K) {
     if (N >= 32768 && M >= 3 && M <= 6) return 5;
     return K <= 8192 ? 8 : 6;
   }
-  if (fmt == F_Q6_K) return K <= 4096 ? 8 : 1;
+  if (fmt == F_Q6_K || fmt == F_Q5_0 || fmt == F_Q8_0) return 8;
   if (fmt == F_MLX) return N >= 12288 ? 8 : 7;
   return 1;
 }
@@ -1225,12 +1229,12 @@ static int mfma_variant(int fmt, int64_t M, int64_t N, int64_t K) {
 hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
                             bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st) {
   if (M == 0 || N == 0) return hipSuccess;
-  // few activation rows on few or unaligned rows: the LDS-staged v_dot2 kernel (weights
-  // read once, decoded once per row and token) beats the MFMA kernels' fixed cost —
-  // measured on the BASELINE decode shapes at M = 2, 4, 8
-  const bool unaligned = fmt == F_Q6_K || fmt == F_Q5_0 || fmt == F_Q8_0;
-  const bool tile_small_m = unaligned ? (M == 2 || M * N <= 8192)
-                                      : fmt == F_Q4_K && M == 2 && (N <= 1024 || a.K >= 8192);
+  // few activation rows on few rows: the LDS-staged v_dot2 kernel (weights read once,
+  // decoded once per row and token) beats the MFMA kernels' fixed cost — measured on
+  // the BASELINE decode shapes at M = 2, 3, 4, 8
+  const bool tile_small_m = fmt == F_Q6_K ? (M == 2 || M * N <= 8192)
+                          : fmt == F_Q5_0 || fmt == F_Q8_0 ? M * N <= 3072
+                          : fmt == F_Q4_K && M == 2 && (N <= 1024 || a.K >= 8192);
   const int v = o.variant ? o.variant : tile_small_m ? 9 : mfma_variant(fmt, M, N, a.K);
   hipError_t e = hipErrorNotSupported;
   if (v == 9) e = launch_gemv_tile(fmt, a, x, x_f32, y, y_f32, M, N, o, st);

@@ -324,6 +324,92 @@ struct XsQ6K {
   }
 };
 
+// GGUF wire Q5_0 / Q8_0 with the weights dequantised to fp16 (d (q - 16) / d q, rounded
+// once).  Unit = 8 blocks of 32 (Q5_0 176 B, Q8_0 272 B: a 16-byte multiple, so with a
+// 4-byte-aligned blob every unit starts 4-byte aligned); lane kq owns blocks 2 kq and
+// 2 kq + 1, read with 16-byte loads from its 4-byte-aligned start and realigned in
+// registers.  Slot S of lane kq holds the lane's elements 8 S .. 8 S + 7 (block S / 4,
+// elements 8 (S % 4) .. + 7) in natural order, so the activations enter the MFMA as
+// loaded (no reorder waits on their loads).
+__device__ __forceinline__ f16x8 xs_x8(__amdgpu_buffer_rsrc_t xr, uint32_t off) {
+  return __builtin_bit_cast(f16x8, bld16(xr, off));
+}
+
+struct XsQ50 {
+  static constexpr int NCH = 8;
+  static constexpr bool WIDE = false;
+  struct Raw { uint32_t w[11]; };
+  __device__ static void load(const Src& src, uint32_t rw, uint32_t, int unit, int kq, Raw& r) {
+    const uint32_t bo = rw + (uint32_t)unit * 176u + 44u * (uint32_t)kq;
+    const u32x4 a = bld16(src.w, bo), b = bld16(src.w, bo + 16u);
+    const auto c = __builtin_amdgcn_raw_buffer_load_b96(src.w, bo + 32u, 0, 0);
+    r.w[0] = a.x; r.w[1] = a.y; r.w[2] = a.z; r.w[3] = a.w;
+    r.w[4] = b.x; r.w[5] = b.y; r.w[6] = b.z; r.w[7] = b.w;
+    r.w[8] = c[0]; r.w[9] = c[1]; r.w[10] = c[2];
+  }
+  __device__ static f16x8 xload(__amdgpu_buffer_rsrc_t xr, uint32_t off, int S, int kq) {
+    return xs_x8(xr, off + 2u * (uint32_t)(64 * kq + 8 * S));
+  }
+  // block A at byte 0: d | qh at 2 | qs at 6; block B at byte 22: d | qh at 24 | qs at 28
+  __device__ static uint32_t qs(const Raw& r, int blk, int i) {
+    return blk ? r.w[7 + i] : __builtin_amdgcn_alignbyte(r.w[2 + i], r.w[1 + i], 2);
+  }
+  __device__ static uint32_t qh(const Raw& r, int blk) {
+    return blk ? r.w[6] : __builtin_amdgcn_alignbyte(r.w[1], r.w[0], 2);
+  }
+  template <int C>
+  __device__ static void dq(const f16x8* xu, const Raw& r, f32x4& acc) {
+    constexpr int blk = C >> 2, j0 = 8 * (C & 3), nsh = 4 * ((C >> 1) & 1), wi = 2 * (C & 1);
+    const float dd = h2f(blk ? r.w[5] >> 16 : r.w[0]), s = dd * 16777216.f, c = -16.f * dd;
+    const uint32_t h = qh(r, blk);
+    uint32_t b[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      // elements (2p, 2p + 1): bytes 2 (p & 1) and + 1 of qs word wi + p / 2, their
+      // nibble at nsh, qh bits j0 + 2p and + 1 moved to bits 4 and 20
+      const uint32_t v = __builtin_amdgcn_perm(0u, qs(r, blk, wi + (p >> 1)), (p & 1) ? 0x0c030c02u : 0x0c010c00u);
+      const uint32_t hb = (__builtin_amdgcn_ubfe(h, j0 + 2 * p, 2) * 0x00080010u) & 0x00100010u;
+      b[p] = xs_dq2(((v >> nsh) & 0x000F000Fu) | hb, s, c);
+    }
+    acc = xs_mfma32(xu[C], u32x4{b[0], b[1], b[2], b[3]}, acc);
+  }
+};
+
+struct XsQ80 {
+  static constexpr int NCH = 8;
+  static constexpr bool WIDE = false;
+  struct Raw { uint32_t w[17]; };
+  __device__ static void load(const Src& src, uint32_t rw, uint32_t, int unit, int kq, Raw& r) {
+    const uint32_t bo = rw + (uint32_t)unit * 272u + 68u * (uint32_t)kq;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 a = bld16(src.w, bo + 16u * i);
+      r.w[4 * i] = a.x; r.w[4 * i + 1] = a.y; r.w[4 * i + 2] = a.z; r.w[4 * i + 3] = a.w;
+    }
+    r.w[16] = bld4(src.w, bo + 64u);
+  }
+  __device__ static f16x8 xload(__amdgpu_buffer_rsrc_t xr, uint32_t off, int S, int kq) {
+    return xs_x8(xr, off + 2u * (uint32_t)(64 * kq + 8 * S));
+  }
+  // block A at byte 0: d | qs at 2; block B at byte 34: d | qs at 36
+  __device__ static uint32_t qs(const Raw& r, int blk, int i) {
+    return blk ? r.w[9 + i] : __builtin_amdgcn_alignbyte(r.w[1 + i], r.w[i], 2);
+  }
+  template <int C>
+  __device__ static void dq(const f16x8* xu, const Raw& r, f32x4& acc) {
+    constexpr int blk = C >> 2, wi = 2 * (C & 3);
+    const float dd = h2f(blk ? r.w[8] >> 16 : r.w[0]), s = dd * 16777216.f, c = -128.f * dd;
+    uint32_t b[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      // int8 q as the byte q + 128 (fp16 denormal (q + 128) 2^-24): elements 2p, 2p + 1
+      const uint32_t v = __builtin_amdgcn_perm(0u, qs(r, blk, wi + (p >> 1)), (p & 1) ? 0x0c030c02u : 0x0c010c00u);
+      b[p] = xs_dq2(v ^ 0x00800080u, s, c);
+    }
+    acc = xs_mfma32(xu[C], u32x4{b[0], b[1], b[2], b[3]}, acc);
+  }
+};
+
 // MLX 4-bit affine with the weights dequantised to fp16 (s q + b, rounded once), any
 // group size 32 << GSH: every lane reads two 16-byte runs of four words (words 4 kq
 // .. + 3 and 16 + 4 kq .. + 3 of the unit; MFMA S takes word 16 (S / 4) + 4 kq + S % 4),
@@ -452,6 +538,7 @@ struct XsJob {
   float* h;                // MODE 1 output
   float* part;             // MODE 2 output
   int W;                   // waves per workgroup (set by the launcher)
+  int kp;                  // K passes (multi-pass kernel; set by the launcher)
 };
 
 // a * b rounded to fp32.  The empty asm (no instruction) pins the fp32 value: without
@@ -474,7 +561,11 @@ __device__ __forceinline__ float xs_act(int act, float v) {
 
 // NS: sub-blocks per wave (8 or 16); TT: token slots folded per lane (lanes 16 kq
 // hold tokens 4 kq .. 4 kq + 3, so at most TT <= 4 active rows need only the first
-// TT); RT: 16-row tiles per reduction.  The tile loop is
+// TT); RT: 16-row tiles per reduction.  MP (MODE 0, RT = 1, dequantising providers):
+// K longer than the W waves' slots is covered in j.kp passes, pass p giving wave w the
+// units (p W + w) UPW ..; the tile's accumulators carry over the passes, the weights
+// of pass p + 1 are requested before pass p is computed and the activations of each
+// pass are loaded after the previous pass's MFMAs.  Otherwise the tile loop is
 // software-pipelined over two register sets: the weights of the workgroup's next
 // RT tiles are requested before the current ones are used (PIPE), and the first
 // tiles' weights are requested before the activations are waited for.  Rows past the
@@ -482,8 +573,9 @@ __device__ __forceinline__ float xs_act(int act, float v) {
 // bounds, no memory traffic); outputs past the valid rows and tokens are not
 // stored.  Dynamic LDS: Xs[W][NS/8][NCH][16] + red[W][RT][64][4 NM] (+ tmx[W][16]
 // + tsc[16] for MODE 2) floats.
-template <class P, int MODE, int NS, int TT, int RT, bool PIPE, class YT>
+template <class P, int MODE, int NS, int TT, int RT, bool PIPE, class YT, bool MP = false>
 __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
+  static_assert(!MP || (MODE == 0 && RT == 1 && !PIPE && XsIsDQ<P>::value), "multi-pass: dense, one tile, dequantising");
   constexpr int NM = (MODE == 1 || MODE == 3) ? 2 : 1;   // weight matrices per output
   constexpr int UPW = NS / 8;                    // units per wave
   constexpr int NCH = P::NCH;                    // chains per unit
@@ -499,8 +591,12 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
   float* tmx = red + W * RT * 64 * 4 * NM;               // [W][16] token |x| maxima (MODE 2)
   float* tsc = tmx + W * 16;                             // [16] token scales (MODE 2)
   const int n16 = lane & 15, kq = lane >> 4;
-  const int u0 = wave * UPW;                             // first unit of this wave
-  const int nu = KU - u0 < UPW ? KU - u0 : UPW;          // units present (uniform)
+  int u0 = wave * UPW;                                   // first unit of this wave (this pass)
+  int nu = KU - u0 < UPW ? KU - u0 : UPW;                // units present (uniform; <= 0: none)
+  auto set_pass = [&](int p) {
+    u0 = (p * W + wave) * UPW;
+    nu = KU - u0 < UPW ? KU - u0 : UPW;
+  };
 
   int cnt = j.M, p0 = 0, tok = 0;
   int64_t row0 = 0;                                      // first weight row of the block
@@ -546,7 +642,10 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
 #pragma unroll
       for (int mi = 0; mi < NM; ++mi) {
 #pragma unroll
-        for (int u = 0; u < UPW; ++u) P::load(src[mi], rw, rs, u0 + u, kq, raw[r][mi][u]);
+        for (int u = 0; u < UPW; ++u) {
+          const bool has = u < nu;                       // units past K: no traffic
+          P::load(src[mi], has ? rw : 0x80000000u, has ? rs : 0x80000000u, u0 + u, kq, raw[r][mi][u]);
+        }
       }
     }
   };
@@ -601,15 +700,10 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
     }
   };
 
-  // fold the tiles t .. t+RT-1 of `raw` (TTR token slots per lane), reduce over the
-  // waves, store
-  auto compute_tiles = [&](const Raw (&raw)[RT][NM][UPW], int t, auto ttc) {
+  // fold tile r of `raw` into acc (TTR token slots per lane)
+  auto accumulate = [&](const Raw (&raw)[RT][NM][UPW], int r, f32x4 (&acc)[NM], auto ttc) {
     constexpr int TTR = decltype(ttc)::value;
-#pragma unroll
-    for (int r = 0; r < RT; ++r) {
-      f32x4 acc[NM];
-#pragma unroll
-      for (int mi = 0; mi < NM; ++mi) acc[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
+    {
 #pragma unroll
       for (int u = 0; u < UPW; ++u) {
         if (u >= nu) break;                      // uniform; keeps xa[] statically indexed
@@ -637,10 +731,16 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
           }
         });
       }
+    }
+  };
+  // reduce the accumulators of tiles t .. t+RT-1 over the waves, store
+  auto finish = [&](const f32x4 (&acc)[RT][NM], int t, auto ttc) {
+    constexpr int TTR = decltype(ttc)::value;
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
 #pragma unroll
       for (int mi = 0; mi < NM; ++mi)
-        *(f32x4*)&red[((wave * RT + r) * 64 + lane) * (4 * NM) + 4 * mi] = acc[mi];
-    }
+        *(f32x4*)&red[((wave * RT + r) * 64 + lane) * (4 * NM) + 4 * mi] = acc[r][mi];
     // LDS-only barriers: a __syncthreads would also wait for the next tiles' weights
     // (its fence drains every outstanding load), serialising the prefetch
     lds_barrier();
@@ -667,9 +767,57 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
     }
     lds_barrier();                                // red[] is reused by the next tiles
   };
+  auto compute_tiles = [&](const Raw (&raw)[RT][NM][UPW], int t, auto ttc) {
+    f32x4 acc[RT][NM];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi) acc[r][mi] = f32x4{0.f, 0.f, 0.f, 0.f};
+      accumulate(raw, r, acc[r], ttc);
+    }
+    finish(acc, t, ttc);
+  };
 
   Raw ra[RT][NM][UPW];
   int t = blockIdx.x * RT;
+  if constexpr (MP) {
+    // every pass computes all of its units: units past K were loaded as zeros (weights
+    // and activations), which adds nothing, and there is no branch between a load and
+    // its use that would make the compiler wait for the newer prefetch too
+    const int KP = j.kp;
+    const std::integral_constant<int, TT> ttc;
+    auto fold = [&](const Raw (&raw)[RT][NM][UPW], f32x4 (&acc)[NM]) {
+#pragma unroll
+      for (int u = 0; u < UPW; ++u)
+#pragma unroll
+        for (int mi = 0; mi < NM; ++mi) P::dq_unit(&xa[8 * u], raw[0][mi][u], acc[mi]);
+    };
+    Raw rc[1][NM][UPW];
+    for (; t < ntiles16; t += stride) {          // uniform
+      f32x4 acc[1][NM];
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi) acc[0][mi] = f32x4{0.f, 0.f, 0.f, 0.f};
+      set_pass(0);
+      load_tiles(ra, t);
+      load_x();
+      // scheduling barriers keep each prefetch issued ahead of the MFMAs of the pass
+      // before it (the waits then count only the older loads)
+      for (int p = 0; p < KP; p += 2) {          // passes in pairs: ra even, rc odd
+        set_pass(p + 1);
+        load_tiles(rc, t);                       // (past the last pass: out of bounds)
+        __builtin_amdgcn_sched_barrier(0);
+        fold(ra, acc[0]);
+        load_x();
+        set_pass(p + 2);
+        load_tiles(ra, t);
+        __builtin_amdgcn_sched_barrier(0);
+        fold(rc, acc[0]);
+        load_x();
+      }
+      finish(acc, t, ttc);
+    }
+    return;
+  }
   if constexpr (XsIsDQ<P>::value) {
     // weights first: the activations' reorder waits for their loads, which then
     // overlap the weights' instead of preceding them
@@ -717,7 +865,8 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
 }
 
 // Host launcher.  hipErrorNotSupported when the shape does not fit the kernel
-// (K not a multiple of 256 or over 8192, offsets of 2 GiB or more): the caller then
+// (K not a multiple of 256, over 8192 except for the multi-pass dense kernel of the
+// dequantising providers, offsets of 2 GiB or more): the caller then
 // uses another kernel.  MODE 0: one 16-row tile (rt = 1) or two (rt = 2) per
 // workgroup while the tiles fit the resident workgroups, else as many workgroups as
 // are resident (or `cap`), each looping over tiles with the next tiles' weights in
@@ -733,11 +882,16 @@ hipError_t launch_xs(const XsJob& j, int64_t tiles_y, int64_t cap, int rt, hipSt
   if (rows * (uint64_t)j.a.rb >= (1ull << 31) || rows * j.sb >= (1ull << 31) || j.xbytes >= (1u << 31))
     return hipErrorNotSupported;
   const int KS = K / 32;
-  const int ns = KS <= 8 * 16 ? 8 : KS <= 16 * 16 ? 16 : 0;   // at most 16 waves
+  int ns = KS <= 8 * 16 ? 8 : KS <= 16 * 16 ? 16 : 0;   // at most 16 waves
+  int kp = 1;
+  if (ns != 8 && MODE == 0 && XsIsDQ<P>::value && !P::WIDE) {
+    ns = 8;                                       // multi-pass: 8 slots per wave, <= 16 waves
+    kp = (KS + 8 * 16 - 1) / (8 * 16);
+  }
   if (!ns || ((NM == 2 || !P::WIDE) && ns == 16)) return hipErrorNotSupported;   // (registers)
   if (!DENSE && tiles_y > 65535) return hipErrorNotSupported;
   if (!DENSE && tiles_y <= 0) return hipSuccess;
-  const int W = (KS + ns - 1) / ns;
+  const int W = (KS + ns * kp - 1) / (ns * kp);
   const int64_t tiles = (j.N + 15) / 16;
   // 16 sub-blocks per wave leave registers for one tile in flight only
   rt = (ns == 16 || MODE != 0 || rt < 2 || !P::WIDE) ? 1 : 2;   // (two tiles: MODE 0 only)
@@ -761,6 +915,7 @@ hipError_t launch_xs(const XsJob& j, int64_t tiles_y, int64_t cap, int rt, hipSt
     const dim3 grid((unsigned)gx, DENSE ? 1u : (unsigned)tiles_y), block((unsigned)(64 * W));
     XsJob jw = j;
     jw.W = W;
+    jw.kp = kp;
     hipLaunchKernelGGL(kern, grid, block, lds, st, jw);
     return hipGetLastError();
   };
@@ -776,6 +931,9 @@ hipError_t launch_xs(const XsJob& j, int64_t tiles_y, int64_t cap, int rt, hipSt
     auto pick = [&](auto ttc, auto yt) -> hipError_t {
       constexpr int TT = decltype(ttc)::value;
       using YT = decltype(yt);
+      if constexpr (XsIsDQ<P>::value && !P::WIDE) {
+        if (kp > 1) return go(k_gemv_xs<P, 0, 8, TT, 1, false, YT, true>, false);
+      }
       if constexpr (P::WIDE) {
         if (ns == 16) return go(k_gemv_xs<P, 0, 16, TT, 1, false, YT>, false);
         if (rt == 2) return go(k_gemv_xs<P, 0, 8, TT, 2, true, YT>, true);

@@ -152,13 +152,32 @@ def test_gemv_mfma(dev, fmt, M):
     for rg in (1, 2):
         y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=rg << 28).cpu().numpy()
         check(y, x, wt.W, f"{fmt} gemv_mfma M={M} rg={rg}")
-    if fmt in ("q4_k", "q6_k", "mlx_q4") and M <= 16:
+    if fmt in ("q4_k", "q6_k", "mlx_q4", "q8_0", "q5_0") and M <= 16:
         # every kernel explicitly: 1 = 16x16x32 tiles, 5 = 4x4x4 broadcast (Q4_K),
         # 6 = x-stationary 16x16x32 (Q4_K), 7 = generic x-stationary (Q4_K, Q6_K, MLX),
-        # 8 = x-stationary with fp16-dequantised weights (Q4_K, Q6_K, MLX)
-        for variant in ((1, 5, 6, 7, 8) if fmt == "q4_k" else (1, 7, 8)):
+        # 8 = x-stationary with fp16-dequantised weights (Q4_K, Q6_K, MLX, Q8_0, Q5_0)
+        variants = {"q4_k": (1, 5, 6, 7, 8), "q8_0": (1, 8), "q5_0": (1, 8)}.get(fmt, (1, 7, 8))
+        for variant in variants:
             y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=variant << 36).cpu().numpy()
             check(y, x, wt.W, f"{fmt} gemv_mfma M={M} variant={variant}")
+
+
+@pytest.mark.parametrize("fmt", ["q6_k", "q5_0", "q8_0"])
+@pytest.mark.parametrize("M", [3, 8, 16])
+@pytest.mark.parametrize("K,N", [(8192, 72), (11008, 33), (14336, 40)])
+def test_gemv_xs_multipass(dev, fmt, M, K, N):
+    """K beyond 16 waves x 8 slots: the dequantising x-stationary kernel in passes over
+    K (2, 3 and 4 passes; the last pass of K = 11008 leaves waves without units, whose
+    loads fall past the row or the buffer and must add nothing); forced and default."""
+    rng = np.random.default_rng(K + N + M)
+    wt = Weight(fmt, N, K, rng, dev)
+    x = synth.numpy_x(M, K, rng)
+    xt = torch.from_numpy(x).to(dev)
+    for opts in (8 << 36, 0):
+        y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=opts).cpu().numpy()
+        check(y, x, wt.W, f"{fmt} xs multi-pass M={M} K={K} N={N} opts={opts:#x}")
+    y16 = wt.qmm(xt, path="gemv_mfma", opts=8 << 36).float().cpu().numpy()
+    check(y16, x, wt.W, f"{fmt} xs multi-pass fp16 out M={M} K={K} N={N}")
 
 
 @pytest.mark.parametrize("fmt", FORMATS)
