@@ -1135,7 +1135,7 @@ static hipError_t launch_gemv_xs(int fmt, const QArgs& a, const void* x, bool x_
     const int64_t dcap = o.grid_cap > 0 ? o.grid_cap : N >= 12288 ? cu_count() : 1024;
     const int rt = o.row_groups ? o.row_groups : fmt == F_Q4_K && M > 8 && N > 4096 && N < 12288 ? 2 : 1;
     if (fmt == F_Q4_K) return launch_xs<XsDQ<XsQ4K>, 0>(j, 0, dcap, rt, st);
-    if (fmt == F_Q6_K) return launch_xs<XsDQ<XsQ6K>, 0>(j, 0, dcap, rt, st);
+    if (fmt == F_Q6_K) return launch_xs<XsDQ<XsQ6KW>, 0>(j, 0, dcap, rt, st);
     if (fmt == F_Q5_0) return launch_xs<XsDQ<XsQ50>, 0>(j, 0, dcap, rt, st);
     if (fmt == F_Q8_0) return launch_xs<XsDQ<XsQ80>, 0>(j, 0, dcap, rt, st);
   } else {
@@ -1232,8 +1232,7 @@ hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, 
   // few activation rows on few rows: the LDS-staged v_dot2 kernel (weights read once,
   // decoded once per row and token) beats the MFMA kernels' fixed cost — measured on
   // the BASELINE decode shapes at M = 2, 3, 4, 8
-  const bool tile_small_m = fmt == F_Q6_K ? (M == 2 || M * N <= 8192)
-                          : fmt == F_Q5_0 || fmt == F_Q8_0 ? M * N <= 3072
+  const bool tile_small_m = fmt == F_Q6_K || fmt == F_Q5_0 || fmt == F_Q8_0 ? M * N <= 3072
                           : fmt == F_Q4_K && M == 2 && (N <= 1024 || a.K >= 8192);
   const int v = o.variant ? o.variant : tile_small_m ? 9 : mfma_variant(fmt, M, N, a.K);
   hipError_t e = hipErrorNotSupported;

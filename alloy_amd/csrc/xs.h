@@ -49,6 +49,11 @@ __device__ __forceinline__ f16x8 xs_x8_perm8(__amdgpu_buffer_rsrc_t xr, uint32_t
   return __builtin_bit_cast(f16x8, u32x4{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
                                          __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)});
 }
+// 8 fp16 activations at byte `off` in natural order
+__device__ __forceinline__ f16x8 xs_x8(__amdgpu_buffer_rsrc_t xr, uint32_t off) {
+  return __builtin_bit_cast(f16x8, bld16(xr, off));
+}
+
 // The four words of a as floats.  Each element is copied to a scalar before the
 // bit cast: a bit cast of a vector element expression itself has produced element 0.
 __device__ __forceinline__ void xs_u4_to_f(u32x4 a, float* f) {
@@ -324,6 +329,75 @@ struct XsQ6K {
   }
 };
 
+// Q6_K with the weights dequantised to fp16 (d sc (q - 32), rounded once), read as
+// wide contiguous runs.  Lane kq owns the 64 elements 128 h + 32 s + l with h = kq / 2
+// and s in {kq % 2, kq % 2 + 2} (l < 32): their low bits are the 32 ql bytes at 32 kq
+// (nibble s / 2), their high bits the 32 qh bytes at 128 + 32 h (bits 2 s), their
+// scales bytes 192 + 8 h + 2 s + l / 16, and d the fp16 at 208.  The unit starts only
+// 2-byte aligned, so each run is loaded from the 4-byte boundary below it (8 loads of
+// 2-16 bytes per unit and lane) and realigned by `sh` bytes when used.  No load that
+// carries needed bytes reaches past the block (a load that only partly fits the buffer
+// reads as zero whole, which would lose data of the buffer's last block): d has a
+// 2-byte load of its own.  Slot S holds elements l = 8 (S % 4) .. + 7 of
+// s = kq % 2 + 2 (S / 4), in natural order.
+struct XsQ6KW {
+  static constexpr int NCH = 8;
+  static constexpr bool WIDE = false;
+  static constexpr int MPW = 8;                  // 24 raw words per unit and buffer
+  struct Raw { uint32_t ql[9], qh[9], sc[3], d, sh; };
+  __device__ static void load(const Src& src, uint32_t rw, uint32_t, int unit, int kq, Raw& r) {
+    const uint32_t bo = rw + (uint32_t)unit * 210u, sh = bo & 2u, base = bo - sh;
+    const uint32_t h = (uint32_t)kq >> 1;
+    const u32x4 a0 = bld16(src.w, base + 32u * kq), a1 = bld16(src.w, base + 32u * kq + 16u);
+    const u32x4 b0 = bld16(src.w, base + 128u + 32u * h), b1 = bld16(src.w, base + 144u + 32u * h);
+    // the scales' run as 8 + 4 bytes: the third word is needed only when sh = 2, and
+    // then it lies inside the block (a load that only partly fits the buffer would
+    // read as zero whole)
+    const uint2 c0 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(src.w, base + 192u + 8u * h, 0, 0));
+    r.ql[0] = a0.x; r.ql[1] = a0.y; r.ql[2] = a0.z; r.ql[3] = a0.w;
+    r.ql[4] = a1.x; r.ql[5] = a1.y; r.ql[6] = a1.z; r.ql[7] = a1.w;
+    r.ql[8] = bld4(src.w, base + 32u * kq + 32u);
+    r.qh[0] = b0.x; r.qh[1] = b0.y; r.qh[2] = b0.z; r.qh[3] = b0.w;
+    r.qh[4] = b1.x; r.qh[5] = b1.y; r.qh[6] = b1.z; r.qh[7] = b1.w;
+    r.qh[8] = bld4(src.w, base + 160u + 32u * h);
+    r.sc[0] = c0.x; r.sc[1] = c0.y; r.sc[2] = bld4(src.w, base + 200u + 8u * h);
+    r.d = bld2(src.w, bo + 208u);
+    r.sh = sh * 8u;                                // as a bit shift
+  }
+  __device__ static uint32_t al(uint32_t hi, uint32_t lo, uint32_t shb) {
+    return (uint32_t)(((uint64_t)hi << 32 | lo) >> shb);
+  }
+  // slot S: elements 128 (kq / 2) + 32 (kq % 2 + 2 (S / 4)) + 8 (S % 4) .. + 7
+  __device__ static f16x8 xload(__amdgpu_buffer_rsrc_t xr, uint32_t off, int S, int kq) {
+    return xs_x8(xr, off + 2u * (uint32_t)(128 * (kq >> 1) + 32 * ((kq & 1) + 2 * (S >> 2)) + 8 * (S & 3)));
+  }
+  __device__ static void xload32(__amdgpu_buffer_rsrc_t xr, uint32_t off, int S, int kq, float (&v)[8]) {
+    xs_x8_f32<0, 1, 2, 3, 4, 5, 6, 7>(xr, off + 4u * (uint32_t)(128 * (kq >> 1) + 32 * ((kq & 1) + 2 * (S >> 2)) + 8 * (S & 3)), v);
+  }
+  template <int C>
+  __device__ static void dq(const f16x8* xu, const Raw& r, f32x4& acc) {
+    constexpr int hi = C >> 2, l0 = 8 * (C & 3), wq = l0 / 4;
+    const uint32_t shb = r.sh;
+    // the lane's kq % 2 (not a template value): s = kq % 2 + 2 hi
+    const uint32_t kq1 = (__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) >> 4) & 1u;
+    const uint32_t qsh = 2u * kq1 + 4u * hi;
+    // realigned scale words: bytes 8 h + 0..3 and + 4..7 of the scales; the slot's
+    // scale is byte 2 (kq % 2) + (l0 >= 16) of word hi
+    const uint32_t scw = hi ? al(r.sc[2], r.sc[1], shb) : al(r.sc[1], r.sc[0], shb);
+    const int scb = __builtin_amdgcn_sbfe((int)scw, (int)(16u * kq1 + (l0 >= 16 ? 8u : 0u)), 8);
+    const float sc = h2f(r.d) * (float)scb, sm = sc * 16777216.f, c = -32.f * sc;
+    uint32_t b[4];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const uint32_t v = al(r.ql[wq + k + 1], r.ql[wq + k], shb), u = al(r.qh[wq + k + 1], r.qh[wq + k], shb);
+      const uint32_t q4 = ((v >> (4 * hi)) & 0x0F0F0F0Fu) | (((u >> qsh) & 0x03030303u) << 4);
+      b[2 * k] = xs_dq2(__builtin_amdgcn_perm(0u, q4, 0x0c010c00u), sm, c);
+      b[2 * k + 1] = xs_dq2(__builtin_amdgcn_perm(0u, q4, 0x0c030c02u), sm, c);
+    }
+    acc = xs_mfma32(xu[C], u32x4{b[0], b[1], b[2], b[3]}, acc);
+  }
+};
+
 // GGUF wire Q5_0 / Q8_0 with the weights dequantised to fp16 (d (q - 16) / d q, rounded
 // once).  Unit = 8 blocks of 32 (Q5_0 176 B, Q8_0 272 B: a 16-byte multiple, so with a
 // 4-byte-aligned blob every unit starts 4-byte aligned); lane kq owns blocks 2 kq and
@@ -331,10 +405,6 @@ struct XsQ6K {
 // registers.  Slot S of lane kq holds the lane's elements 8 S .. 8 S + 7 (block S / 4,
 // elements 8 (S % 4) .. + 7) in natural order, so the activations enter the MFMA as
 // loaded (no reorder waits on their loads).
-__device__ __forceinline__ f16x8 xs_x8(__amdgpu_buffer_rsrc_t xr, uint32_t off) {
-  return __builtin_bit_cast(f16x8, bld16(xr, off));
-}
-
 struct XsQ50 {
   static constexpr int NCH = 8;
   static constexpr bool WIDE = false;
@@ -505,6 +575,13 @@ struct XsDQ : P {
     xs_static_for<0, P::NCH>([&](auto cc) { P::template dq<decltype(cc)::value>(xu, r, acc); });
   }
 };
+// Waves per workgroup of the multi-pass kernel (MP): 16 by default (activations of a
+// pass loaded after the previous pass's MFMAs, 128 VGPRs), 8 for providers whose raw
+// bytes need the 256 VGPRs of an 8-wave workgroup (activations double-buffered too).
+template <class P, class = void>
+struct XsMPW : std::integral_constant<int, 16> {};
+template <class P>
+struct XsMPW<P, std::void_t<decltype(P::MPW)>> : std::integral_constant<int, P::MPW> {};
 template <class P, class = void>
 struct XsIsDQ : std::false_type {};
 template <class P>
@@ -561,11 +638,11 @@ __device__ __forceinline__ float xs_act(int act, float v) {
 
 // NS: sub-blocks per wave (8 or 16); TT: token slots folded per lane (lanes 16 kq
 // hold tokens 4 kq .. 4 kq + 3, so at most TT <= 4 active rows need only the first
-// TT); RT: 16-row tiles per reduction.  MP (MODE 0, RT = 1, dequantising providers):
-// K longer than the W waves' slots is covered in j.kp passes, pass p giving wave w the
-// units (p W + w) UPW ..; the tile's accumulators carry over the passes, the weights
-// of pass p + 1 are requested before pass p is computed and the activations of each
-// pass are loaded after the previous pass's MFMAs.  Otherwise the tile loop is
+// TT); RT: 16-row tiles per reduction.  MP (MODE 0, RT = 1, dequantising providers,
+// at most XsMPW waves): K longer than the W waves' slots is covered in j.kp passes,
+// pass p giving wave w the units (p W + w) UPW ..; the tile's accumulators carry over
+// the passes, and the weights of pass p + 1 are requested before pass p is computed.
+// Otherwise the tile loop is
 // software-pipelined over two register sets: the weights of the workgroup's next
 // RT tiles are requested before the current ones are used (PIPE), and the first
 // tiles' weights are requested before the activations are waited for.  Rows past the
@@ -574,7 +651,7 @@ __device__ __forceinline__ float xs_act(int act, float v) {
 // stored.  Dynamic LDS: Xs[W][NS/8][NCH][16] + red[W][RT][64][4 NM] (+ tmx[W][16]
 // + tsc[16] for MODE 2) floats.
 template <class P, int MODE, int NS, int TT, int RT, bool PIPE, class YT, bool MP = false>
-__global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
+__global__ __launch_bounds__(MP ? 64 * XsMPW<P>::value : 1024) void k_gemv_xs(XsJob j) {
   static_assert(!MP || (MODE == 0 && RT == 1 && !PIPE && XsIsDQ<P>::value), "multi-pass: dense, one tile, dequantising");
   constexpr int NM = (MODE == 1 || MODE == 3) ? 2 : 1;   // weight matrices per output
   constexpr int UPW = NS / 8;                    // units per wave
@@ -653,7 +730,7 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
   // A operands: token slot n16, slots 8 u .. 8 u + 7 of unit u0 + u (provider order)
   f16x8 xa[NS];
   constexpr uint32_t XB = MODE == 2 ? 4u : 2u;           // bytes per activation
-  auto load_x = [&]() {
+  auto load_x_to = [&](f16x8 (&xa)[NS]) {
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)j.x, (short)0, (int)j.xbytes, ALLOY_RSRC_DW3);
     uint32_t xrow = 0x80000000u;                         // past the buffer: zeros
     if (n16 < cnt) {
@@ -699,6 +776,8 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
       }
     }
   };
+
+  auto load_x = [&]() { load_x_to(xa); };
 
   // fold tile r of `raw` into acc (TTR token slots per lane)
   auto accumulate = [&](const Raw (&raw)[RT][NM][UPW], int r, f32x4 (&acc)[NM], auto ttc) {
@@ -783,36 +862,59 @@ __global__ __launch_bounds__(1024) void k_gemv_xs(XsJob j) {
   if constexpr (MP) {
     // every pass computes all of its units: units past K were loaded as zeros (weights
     // and activations), which adds nothing, and there is no branch between a load and
-    // its use that would make the compiler wait for the newer prefetch too
+    // its use that would make the compiler wait for the newer prefetch too.  Weights
+    // alternate between ra and rc, one pass ahead; with 8 waves the activations too
+    // (xa / xb), with 16 they are loaded after the previous pass's MFMAs.
+    // Scheduling barriers keep each prefetch issued ahead of the MFMAs of the pass
+    // before it (the waits then count only the older loads); passes past the last load
+    // out of bounds (no traffic).
     const int KP = j.kp;
     const std::integral_constant<int, TT> ttc;
-    auto fold = [&](const Raw (&raw)[RT][NM][UPW], f32x4 (&acc)[NM]) {
+    constexpr bool X2 = XsMPW<P>::value <= 8;
+    auto fold = [&](const Raw (&raw)[RT][NM][UPW], const f16x8 (&xv)[NS], f32x4 (&acc)[NM]) {
 #pragma unroll
       for (int u = 0; u < UPW; ++u)
 #pragma unroll
-        for (int mi = 0; mi < NM; ++mi) P::dq_unit(&xa[8 * u], raw[0][mi][u], acc[mi]);
+        for (int mi = 0; mi < NM; ++mi) P::dq_unit(&xv[8 * u], raw[0][mi][u], acc[mi]);
     };
     Raw rc[1][NM][UPW];
+    f16x8 xb[X2 ? NS : 1];
     for (; t < ntiles16; t += stride) {          // uniform
       f32x4 acc[1][NM];
 #pragma unroll
       for (int mi = 0; mi < NM; ++mi) acc[0][mi] = f32x4{0.f, 0.f, 0.f, 0.f};
       set_pass(0);
       load_tiles(ra, t);
-      load_x();
-      // scheduling barriers keep each prefetch issued ahead of the MFMAs of the pass
-      // before it (the waits then count only the older loads)
-      for (int p = 0; p < KP; p += 2) {          // passes in pairs: ra even, rc odd
-        set_pass(p + 1);
-        load_tiles(rc, t);                       // (past the last pass: out of bounds)
-        __builtin_amdgcn_sched_barrier(0);
-        fold(ra, acc[0]);
-        load_x();
-        set_pass(p + 2);
-        load_tiles(ra, t);
-        __builtin_amdgcn_sched_barrier(0);
-        fold(rc, acc[0]);
-        load_x();
+      load_x_to(xa);
+      if constexpr (X2) {
+        set_pass(1);
+        load_tiles(rc, t);
+        load_x_to(xb);
+        for (int p = 0; p < KP; p += 2) {        // passes in pairs: (ra, xa) even, (rc, xb) odd
+          __builtin_amdgcn_sched_barrier(0);
+          fold(ra, xa, acc[0]);
+          set_pass(p + 2);
+          load_tiles(ra, t);
+          load_x_to(xa);
+          __builtin_amdgcn_sched_barrier(0);
+          fold(rc, xb, acc[0]);
+          set_pass(p + 3);
+          load_tiles(rc, t);
+          load_x_to(xb);
+        }
+      } else {
+        for (int p = 0; p < KP; p += 2) {        // passes in pairs: ra even, rc odd
+          set_pass(p + 1);
+          load_tiles(rc, t);
+          __builtin_amdgcn_sched_barrier(0);
+          fold(ra, xa, acc[0]);
+          load_x_to(xa);
+          set_pass(p + 2);
+          load_tiles(ra, t);
+          __builtin_amdgcn_sched_barrier(0);
+          fold(rc, xa, acc[0]);
+          load_x_to(xa);
+        }
       }
       finish(acc, t, ttc);
     }
@@ -885,8 +987,9 @@ hipError_t launch_xs(const XsJob& j, int64_t tiles_y, int64_t cap, int rt, hipSt
   int ns = KS <= 8 * 16 ? 8 : KS <= 16 * 16 ? 16 : 0;   // at most 16 waves
   int kp = 1;
   if (ns != 8 && MODE == 0 && XsIsDQ<P>::value && !P::WIDE) {
-    ns = 8;                                       // multi-pass: 8 slots per wave, <= 16 waves
-    kp = (KS + 8 * 16 - 1) / (8 * 16);
+    constexpr int mw = XsMPW<P>::value;          // multi-pass: 8 slots per wave, <= mw waves
+    ns = 8;
+    kp = (KS + 8 * mw - 1) / (8 * mw);
   }
   if (!ns || ((NM == 2 || !P::WIDE) && ns == 16)) return hipErrorNotSupported;   // (registers)
   if (!DENSE && tiles_y > 65535) return hipErrorNotSupported;
