@@ -237,6 +237,11 @@ __global__ __launch_bounds__(256) void k_gemv_w(WaveBatchT<NB> bt, uint32_t sb, 
   float xg[UPT][F::UE / 16];
 #pragma unroll
   for (int j = 0; j < UPT; ++j) load_x_unit<F, f16>(xl, uu[j], xr[j], xg[j]);
+  const bool odd = li & 1;
+  if constexpr (HasPairDot<F>::value) {
+#pragma unroll
+    for (int j = 0; j < UPT; ++j) F::pair_x_sums(xg[j], odd);
+  }
 
   for (int base = bx * R; base < N; base += D * stride) {
 #pragma unroll
@@ -250,8 +255,12 @@ __global__ __launch_bounds__(256) void k_gemv_w(WaveBatchT<NB> bt, uint32_t sb, 
 #pragma unroll
       for (int j = 0; j < UPT; ++j) {
         if constexpr (HasShare<F>::value) F::share(ring[d][j]);
-        const float v = F::dot(ring[d][j], uu[j], xr[j], xg[j]);
-        acc += own[j] ? v : 0.f;
+        if constexpr (HasPairDot<F>::value) {
+          acc += F::dot_pair(ring[d][j], uu[j], xr[j], xg[j], odd);   // (units past the row add 0)
+        } else {
+          const float v = F::dot(ring[d][j], uu[j], xr[j], xg[j]);
+          acc += own[j] ? v : 0.f;
+        }
       }
       const uint32_t nw = rw + (d + D) * dw, ns = rs + (d + D) * ds;
 #pragma unroll

@@ -15,6 +15,11 @@ template <class F, class = void>
 struct HasShare : std::false_type {};
 template <class F>
 struct HasShare<F, std::void_t<decltype(F::share(std::declval<typename F::Raw&>()))>> : std::true_type {};
+// Formats with a pair-split dot for the wave-row GEMV (F::dot_pair, F::pair_x_sums).
+template <class F, class = void>
+struct HasPairDot : std::false_type {};
+template <class F>
+struct HasPairDot<F, std::void_t<decltype(F::pair_x_sums((float*)nullptr, false))>> : std::true_type {};
 
 // Workgroup barriers that order LDS only (lgkmcnt(0) before s_barrier, nothing
 // else), so global loads still in flight (a GEMV's weight prefetch) are not drained

@@ -243,12 +243,13 @@ struct FQ4K {
     r.q = bld16<kStream>(src.w, wo + 16 + 16 * (u & 7));
     return r;
   }
+  // (every lane of the quad is a valid source, so the moves need no old value)
   __device__ static void share(Raw& r) {
     const int v = (int)r.h.x;
-    r.h = u32x4{(uint32_t)__builtin_amdgcn_update_dpp(0, v, 0x00, 0xF, 0xF, false),    // quad_perm [0,0,0,0]
-                (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0x55, 0xF, 0xF, false),    // [1,1,1,1]
-                (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0xAA, 0xF, 0xF, false),    // [2,2,2,2]
-                (uint32_t)__builtin_amdgcn_update_dpp(0, v, 0xFF, 0xF, 0xF, false)};   // [3,3,3,3]
+    r.h = u32x4{(uint32_t)__builtin_amdgcn_mov_dpp(v, 0x00, 0xF, 0xF, true),    // quad_perm [0,0,0,0]
+                (uint32_t)__builtin_amdgcn_mov_dpp(v, 0x55, 0xF, 0xF, true),    // [1,1,1,1]
+                (uint32_t)__builtin_amdgcn_mov_dpp(v, 0xAA, 0xF, 0xF, true),    // [2,2,2,2]
+                (uint32_t)__builtin_amdgcn_mov_dpp(v, 0xFF, 0xF, 0xF, true)};   // [3,3,3,3]
   }
   // Quants enter v_dot2 as fp16 mantissa fields of 1.0: a low nibble (bits 0-3 of a
   // half) reads 1 + q/1024, a high nibble (bits 4-7) 1 + q/64, so one v_bfi_b32
@@ -275,6 +276,43 @@ struct FQ4K {
     const float cA = 1024.f * d * (float)scA, cB = 64.f * d * (float)scB;
     // w = d sc q - dmin m
     return cA * (SA - xg[0]) + cB * (SB - xg[1]) - dmin * ((float)mA * xg[0] + (float)mB * xg[1]);
+  }
+  // Wave-row GEMV with units u = lane + L j (L even): lanes 2i and 2i + 1 hold the two
+  // halves (elements 0-15, 16-31) of the same sub-block pair (2p, 2p + 1).  They add
+  // their sums across the pair (DPP) and each applies one sub-block's scale and min —
+  // sub-block u % 8: the even lane 2p (low nibbles), the odd lane 2p + 1 (high) — so
+  // the scale work per unit is halved.  xgp[0]: the pair's activation sum of this
+  // lane's sub-block (pair_x_sums); units past the row read zero headers and add 0.
+  __device__ static float dot_pair(const Raw& r, int u, const uint32_t* xa, const float* xgp, bool odd) {
+    const uint32_t words[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+    const uint32_t* xb = xa + 8;
+    const uint32_t magic = MAGIC1;
+    float SA = 0.f, SB = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t v = words[i], v8 = v >> 8;
+      SA = dot2(bfi(0x000F000Fu, v, magic), xa[2 * i], SA);
+      SA = dot2(bfi(0x000F000Fu, v8, magic), xa[2 * i + 1], SA);
+      SB = dot2(bfi(0x00F000F0u, v, magic), xb[2 * i], SB);
+      SB = dot2(bfi(0x00F000F0u, v8, magic), xb[2 * i + 1], SB);
+    }
+    const float PA = SA + pair_swap(SA), PB = SB + pair_swap(SB);
+    const float S = odd ? PB : PA, xs = xgp[0];
+    uint32_t sc, m;
+    Q4kSel(u & 7).get(r.h.y, r.h.z, r.h.w, sc, m);
+    const float d = h2f(r.h.x), dmin = h2f(r.h.x >> 16);
+    const float c = (odd ? 64.f : 1024.f) * d * (float)sc;
+    return c * (S - xs) - dmin * (float)m * xs;
+  }
+  // the value of lane l ^ 1 (quad_perm [1,0,3,2])
+  __device__ static float pair_swap(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+  }
+  // xg of the pair_dot layout: xg[0] = the activation sum of the lane's sub-block
+  // (2p for the even lane, 2p + 1 for the odd one) over both halves of the pair
+  __device__ static void pair_x_sums(float* xg, bool odd) {
+    const float a = xg[0] + pair_swap(xg[0]), b = xg[1] + pair_swap(xg[1]);
+    xg[0] = odd ? b : a;
   }
 };
 
