@@ -566,7 +566,7 @@ def main():
         "dtype": "q4_k weights x fp16 activations, fp32 accumulate",
         "data": "synthetic (BASELINE config 2 distributions), weights resident in HBM",
         "config": {"workload": "Llama-3.2-3B Q4_K decode step, M=1: 28 layers x (q,k,v,o,gate,up,down) + lm_head",
-                   "launches_per_step": launches, "weight_bytes_per_step": total_bytes,
+                   "launches_per_step": len(mats), "weight_bytes_per_step": total_bytes,
                    "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4)},
         "roofline": roof,
         "cpu_baseline": cpu,
