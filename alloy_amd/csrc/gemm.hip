@@ -374,6 +374,384 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, 
     }
 }
 
+// ------------------------------------------------------------------ other formats' prefill GEMM
+// The Q4_K kernel's structure (swizzled unpadded LDS tiles, x copied to LDS by the
+// buffer unit two steps ahead through three stages, raw weight bytes in a three-slot
+// register ring three steps ahead, one barrier per 64-element K step) with the weight
+// bytes read and decoded by a per-format provider W.  Weight tile rows are 256 wide
+// (QBN = 256): thread tid serves row tid % 256 and elements 32 h .. 32 h + 31 of each
+// step, h = tid / 256 (uniform per wave), and writes them as four 16-byte chunks.
+//   W::NL                  loads per step and thread (issued whatever the data, so
+//                          the barrier's load count is a constant)
+//   W::Raw, W::load(s, r, kt, h, valid, raw)   the bytes of row r for step kt (valid
+//                          false: out-of-range offsets, zeros, no traffic)
+//   W::decode<CH>(raw, h, o, kt)  chunk CH (elements 8 CH .. 8 CH + 7) of the 32
+//                          weights as fp16 (exact value rounded once), o[i] = elements
+//                          8 CH + 2i, + 1
+// No load that carries needed bytes reaches past its block: a load that only partly
+// fits the buffer reads as zero as a whole.
+struct GemmArgs {                  // one matrix: buffers, their byte sizes, per-row strides
+  const void *w, *aux, *s, *b;
+  uint32_t wbytes, sbytes;         // bytes of w (and aux) / of s and b (0: absent)
+  uint32_t rb, sb;                 // bytes per row of w (and aux) / of s and b
+};
+struct GemmRows {                  // the same as buffer views (built on the device)
+  __amdgpu_buffer_rsrc_t w, aux, s, b;
+  uint32_t rb, sb;
+  __device__ explicit GemmRows(const GemmArgs& g) {
+    w = __builtin_amdgcn_make_buffer_rsrc((void*)g.w, (short)0, (int)g.wbytes, ALLOY_RSRC_DW3);
+    aux = __builtin_amdgcn_make_buffer_rsrc((void*)g.aux, (short)0, g.aux ? (int)g.wbytes : 0, ALLOY_RSRC_DW3);
+    s = __builtin_amdgcn_make_buffer_rsrc((void*)g.s, (short)0, g.s ? (int)g.sbytes : 0, ALLOY_RSRC_DW3);
+    b = __builtin_amdgcn_make_buffer_rsrc((void*)g.b, (short)0, g.b ? (int)g.sbytes : 0, ALLOY_RSRC_DW3);
+    rb = g.rb;
+    sb = g.sb;
+  }
+};
+// two elements as fp16 denormals (integers < 1024 in the halves of v) -> RN16(v * s + c)
+__device__ __forceinline__ uint32_t gw_dq2(uint32_t v, float s, float c) { return xs_dq2(v, s, c); }
+
+// Q8_0 wire blocks (34 B: fp16 d | 32 int8): thread h decodes block 2 kt + h of its row
+// (rows are 68 K / 64 bytes, so the pair of blocks starts 4-byte aligned).  Block 0 is
+// read as 16 + 16 + 2 bytes from its start (quants realigned by 2 bytes), block 1 (2
+// bytes past a 4-byte boundary) as d then 16 + 16 aligned quant bytes: the same three
+// load sizes at per-thread offsets, all inside the block.
+struct GWQ80 {
+  static constexpr int NL = 3;
+  struct Raw { u32x4 a, b; uint32_t t; };
+  __device__ static void load(const GemmRows& s, uint32_t row, int kt, int h, bool valid, Raw& r) {
+    const uint32_t bo = valid ? row * s.rb + 68u * (uint32_t)kt + 34u * (uint32_t)h : kOOB;
+    r.a = bld16(s.w, bo + (h ? 2u : 0u));
+    r.b = bld16(s.w, bo + (h ? 18u : 16u));
+    r.t = bld2(s.w, bo + (h ? 0u : 32u));
+  }
+  template <int CH>
+  __device__ static void decode(const Raw& r, int h, uint32_t (&o)[4], int) {
+    const uint32_t w[9] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.t};
+    const float d = h2f(h ? r.t : r.a.x), s = d * 16777216.f, c = -128.f * d;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      // quant bytes 4i .. 4i + 3: block 0 at bytes 2 + 4i of its run, block 1 aligned
+      constexpr int i0 = 2 * CH;
+      const int i = i0 + k;
+      const uint32_t q = (h ? w[i] : __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2)) ^ 0x80808080u;
+      o[2 * k] = gw_dq2(__builtin_amdgcn_perm(0u, q, 0x0c010c00u), s, c);
+      o[2 * k + 1] = gw_dq2(__builtin_amdgcn_perm(0u, q, 0x0c030c02u), s, c);
+    }
+  }
+};
+
+// Q5_0 wire blocks (22 B: fp16 d | u32 qh | qs[16]): thread h decodes block 2 kt + h
+// (rows are 44 K / 64 bytes).  Block 0 (4-byte aligned) is read as 16 + 4 + 2 bytes
+// and realigned; block 1 (2 bytes past a boundary) as d, then qh and qs aligned.
+struct GWQ50 {
+  static constexpr int NL = 3;
+  struct Raw { u32x4 a; uint32_t m, t; };
+  __device__ static void load(const GemmRows& s, uint32_t row, int kt, int h, bool valid, Raw& r) {
+    const uint32_t bo = valid ? row * s.rb + 44u * (uint32_t)kt + 22u * (uint32_t)h : kOOB;
+    r.a = bld16(s.w, bo + (h ? 6u : 0u));     // block 1: qs
+    r.m = bld4(s.w, bo + (h ? 2u : 16u));     // block 1: qh
+    r.t = bld2(s.w, bo + (h ? 0u : 20u));     // block 1: d
+  }
+  template <int CH>
+  __device__ static void decode(const Raw& r, int h, uint32_t (&o)[4], int) {
+    const float d = h2f(h ? r.t : r.a.x), s = d * 16777216.f, c = -16.f * d;
+    const uint32_t hq = h ? r.m : __builtin_amdgcn_alignbyte(r.a.y, r.a.x, 2);
+    const uint32_t qs[4] = {h ? r.a.x : __builtin_amdgcn_alignbyte(r.a.z, r.a.y, 2),
+                            h ? r.a.y : __builtin_amdgcn_alignbyte(r.a.w, r.a.z, 2),
+                            h ? r.a.z : __builtin_amdgcn_alignbyte(r.m, r.a.w, 2),
+                            h ? r.a.w : __builtin_amdgcn_alignbyte(r.t, r.m, 2)};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      // elements 2p, 2p + 1 (p = 4 CH + k): low (p < 8) or high nibbles of qs bytes
+      // 2p % 16, + 1, and qh bits 2p, 2p + 1 moved to bits 4 and 20
+      const int p = 4 * CH + k, e = 2 * p, j = e & 15;
+      const uint32_t v = __builtin_amdgcn_perm(0u, qs[j >> 2], (j & 2) ? 0x0c030c02u : 0x0c010c00u) >> (e >= 16 ? 4 : 0);
+      const uint32_t hb = (__builtin_amdgcn_ubfe(hq, e, 2) * 0x00080010u) & 0x00100010u;
+      o[k] = gw_dq2((v & 0x000F000Fu) | hb, s, c);
+    }
+  }
+};
+
+// MLX 4-bit affine (qweight u8 [N, K/2], 8 nibbles per word, low first; fp16 scales /
+// biases [N, K/gs], gs a multiple of 32): thread h's 32 elements are 16 qweight bytes
+// of one group
+struct GWMLX {
+  static constexpr int NL = 3;
+  static constexpr double R128 = 0.55;           // 128x256 rate / 256x256 rate (measured)
+  struct Raw { u32x4 q; uint32_t s, b; };
+  __device__ static void load(const GemmRows& s, uint32_t row, int kt, int h, bool valid, Raw& r, int gs) {
+    const uint32_t e0 = 64u * (uint32_t)kt + 32u * (uint32_t)h;
+    r.q = bld16(s.w, valid ? row * s.rb + e0 / 2u : kOOB);
+    const uint32_t so = valid ? row * s.sb + 2u * (e0 / (uint32_t)gs) : kOOB;
+    r.s = bld2(s.s, so);
+    r.b = bld2(s.b, so);
+  }
+  template <int CH>
+  __device__ static void decode(const Raw& r, int, uint32_t (&o)[4], int) {
+    const float sc = h2f(r.s), s = sc * 16777216.f, c = h2f(r.b);
+    const uint32_t v = CH == 0 ? r.q.x : CH == 1 ? r.q.y : CH == 2 ? r.q.z : r.q.w;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      // elements 8 CH + 2p, + 1: nibbles 2p, 2p + 1 of word CH
+      const uint32_t lo = __builtin_amdgcn_ubfe(v, 8 * p, 4), hi = __builtin_amdgcn_ubfe(v, 8 * p + 4, 4);
+      o[p] = gw_dq2(lo | (hi << 16), s, c);
+    }
+  }
+};
+
+// Q8_0 split layout (qweight int8 [N, K], fp16 scales [N, K/32])
+struct GWQ80S {
+  static constexpr int NL = 3;
+  struct Raw { u32x4 a, b; uint32_t d; };
+  __device__ static void load(const GemmRows& s, uint32_t row, int kt, int h, bool valid, Raw& r) {
+    const uint32_t e0 = 64u * (uint32_t)kt + 32u * (uint32_t)h;
+    const uint32_t wo = valid ? row * s.rb + e0 : kOOB;
+    r.a = bld16(s.w, wo);
+    r.b = bld16(s.w, wo + 16u);
+    r.d = bld2(s.s, valid ? row * s.sb + 2u * (e0 / 32u) : kOOB);
+  }
+  template <int CH>
+  __device__ static void decode(const Raw& r, int, uint32_t (&o)[4], int) {
+    const float d = h2f(r.d), s = d * 16777216.f, c = -128.f * d;
+    const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const uint32_t q = w[2 * CH + k] ^ 0x80808080u;
+      o[2 * k] = gw_dq2(__builtin_amdgcn_perm(0u, q, 0x0c010c00u), s, c);
+      o[2 * k + 1] = gw_dq2(__builtin_amdgcn_perm(0u, q, 0x0c030c02u), s, c);
+    }
+  }
+};
+
+// Q5_0 split layout (qweight u8 [N, K/2]: byte j holds elements 2j (low nibble) and
+// 2j + 1 (high); qhigh u8 [N, K/2]: their fifth bits in bits 0 and 4; fp16 scales)
+struct GWQ50S {
+  static constexpr int NL = 3;
+  static constexpr int MAXMI = 2;                // (a 256x256 tile spills)
+  struct Raw { u32x4 q, hq; uint32_t d; };
+  __device__ static void load(const GemmRows& s, uint32_t row, int kt, int h, bool valid, Raw& r) {
+    const uint32_t e0 = 64u * (uint32_t)kt + 32u * (uint32_t)h;
+    const uint32_t wo = valid ? row * s.rb + e0 / 2u : kOOB;
+    r.q = bld16(s.w, wo);
+    r.hq = bld16(s.aux, wo);
+    r.d = bld2(s.s, valid ? row * s.sb + 2u * (e0 / 32u) : kOOB);
+  }
+  template <int CH>
+  __device__ static void decode(const Raw& r, int, uint32_t (&o)[4], int) {
+    const float d = h2f(r.d), s = d * 16777216.f, c = -16.f * d;
+    const uint32_t q = CH == 0 ? r.q.x : CH == 1 ? r.q.y : CH == 2 ? r.q.z : r.q.w;
+    const uint32_t hq = CH == 0 ? r.hq.x : CH == 1 ? r.hq.y : CH == 2 ? r.hq.z : r.hq.w;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      // elements 8 CH + 2p, + 1 from byte p of word CH: (lo nibble | bit 0 << 4, hi nibble | bit 4)
+      const uint32_t lo = __builtin_amdgcn_ubfe(q, 8 * p, 4) | (__builtin_amdgcn_ubfe(hq, 8 * p, 1) << 4);
+      const uint32_t hi = __builtin_amdgcn_ubfe(q, 8 * p + 4, 4) | (__builtin_amdgcn_ubfe(hq, 8 * p + 4, 1) << 4);
+      o[p] = gw_dq2(lo | (hi << 16), s, c);
+    }
+  }
+};
+
+// Q6_K wire blocks (210 B per 256): step kt is quarter j = kt % 4 of super-block kt / 4,
+// elements 128 hh + 32 s + l with hh = j / 2 and s = 2 (j % 2) + t; thread h takes
+// t = h: low bits = 32 ql bytes at 64 hh + 32 h (nibble j % 2), high bits = 32 qh
+// bytes at 128 + 32 hh (bits 2 s), scales bytes 192 + 8 hh + 2 s (+1 for l >= 16), d
+// at 208.  The runs are loaded from the 4-byte boundary below them and realigned.
+struct GWQ6K {
+  static constexpr int NL = 8;
+  static constexpr int MAXMI = 2;                // (a 256x256 tile spills)
+  struct Raw { uint32_t ql[9], qh[9], sc, d, sh; };
+  __device__ static void load(const GemmRows& s, uint32_t row, int kt, int h, bool valid, Raw& r) {
+    const uint32_t j = (uint32_t)kt & 3u, hh = j >> 1;
+    const uint32_t bo = row * s.rb + 210u * ((uint32_t)kt >> 2), sh = bo & 2u;
+    const uint32_t base = valid ? bo - sh : kOOB;
+    const uint32_t qo = base + 64u * hh + 32u * (uint32_t)h, ho = base + 128u + 32u * hh;
+    const u32x4 a0 = bld16(s.w, qo), a1 = bld16(s.w, qo + 16u);
+    const u32x4 b0 = bld16(s.w, ho), b1 = bld16(s.w, ho + 16u);
+    r.ql[0] = a0.x; r.ql[1] = a0.y; r.ql[2] = a0.z; r.ql[3] = a0.w;
+    r.ql[4] = a1.x; r.ql[5] = a1.y; r.ql[6] = a1.z; r.ql[7] = a1.w;
+    r.ql[8] = bld4(s.w, qo + 32u);
+    r.qh[0] = b0.x; r.qh[1] = b0.y; r.qh[2] = b0.z; r.qh[3] = b0.w;
+    r.qh[4] = b1.x; r.qh[5] = b1.y; r.qh[6] = b1.z; r.qh[7] = b1.w;
+    r.qh[8] = bld4(s.w, ho + 32u);
+    const uint32_t so = valid ? bo + 192u + 8u * hh + 4u * (j & 1u) + 2u * (uint32_t)h : kOOB;
+    r.sc = bld2(s.w, so);
+    r.d = bld2(s.w, valid ? bo + 208u : kOOB);
+    r.sh = 8u * sh;
+  }
+  __device__ static uint32_t al(uint32_t hi, uint32_t lo, uint32_t shb) {
+    return (uint32_t)(((uint64_t)hi << 32 | lo) >> shb);
+  }
+  template <int CH>
+  __device__ static void decode(const Raw& r, int h, uint32_t (&o)[4], int kt) {
+    const uint32_t j = (uint32_t)kt & 3u, s6 = 2u * (j & 1u) + (uint32_t)h;
+    const uint32_t nsh = 4u * (j & 1u), qsh = 2u * s6;
+    // l < 16 (chunks 0, 1): the first of the two scales
+    const float sc = h2f(r.d) * (float)(int8_t)((r.sc >> (CH < 2 ? 0 : 8)) & 0xFFu);
+    const float sm = sc * 16777216.f, c = -32.f * sc;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      constexpr int i0 = 2 * CH;
+      const int i = i0 + k;
+      const uint32_t v = al(r.ql[i + 1], r.ql[i], r.sh), u = al(r.qh[i + 1], r.qh[i], r.sh);
+      const uint32_t q4 = ((v >> nsh) & 0x0F0F0F0Fu) | (((u >> qsh) & 0x03030303u) << 4);
+      o[2 * k] = gw_dq2(__builtin_amdgcn_perm(0u, q4, 0x0c010c00u), sm, c);
+      o[2 * k + 1] = gw_dq2(__builtin_amdgcn_perm(0u, q4, 0x0c030c02u), sm, c);
+    }
+  }
+};
+
+// largest tile row factor (64 MI rows) a provider's registers allow: 4 unless stated
+template <class W, class = void>
+struct GwMaxMi : std::integral_constant<int, 4> {};
+template <class W>
+struct GwMaxMi<W, std::void_t<decltype(W::MAXMI)>> : std::integral_constant<int, W::MAXMI> {};
+
+// a provider's 128x256-tile rate relative to its 256x256 tile: 0.79 unless stated
+template <class W, class = void>
+struct GwR128 { static constexpr double value = 0.79; };
+template <class W>
+struct GwR128<W, std::void_t<decltype(W::R128)>> { static constexpr double value = W::R128; };
+
+// provider load shim (MLX needs the group size)
+template <class W>
+__device__ __forceinline__ void gw_load(const GemmRows& s, uint32_t row, int kt, int h, bool valid,
+                                        typename W::Raw& r, int gs) {
+  if constexpr (std::is_same<W, GWMLX>::value) W::load(s, row, kt, h, valid, r, gs);
+  else W::load(s, row, kt, h, valid, r);
+}
+
+template <class W, int MI, typename YT>
+__global__ __launch_bounds__(512) void k_gemm_w(GemmArgs ga, const f16* x, int M, YT* y, int N, int K, int gs) {
+  const GemmRows g(ga);
+  constexpr int QBM = 64 * MI, QBN = 256, NI = 2;
+  __shared__ __attribute__((aligned(1024))) uint8_t xs0[QBM * 128], xs1[QBM * 128], xs2[QBM * 128];
+  __shared__ __attribute__((aligned(1024))) uint8_t ws0[QBN * 128], ws1[QBN * 128];
+  uint8_t* const XS[3] = {xs0, xs1, xs2};
+  uint8_t* const WS[2] = {ws0, ws1};
+  const int KT = K / 64;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int m0 = (int)blockIdx.y * QBM, n0 = (int)blockIdx.x * QBN;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)x, (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), ALLOY_RSRC_DW3);
+
+  uint32_t xoff[MI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+    const int r = 8 * (MI * wave + i) + (lane >> 3), c = (lane & 7) ^ lds_swz(r);
+    xoff[i] = ((uint32_t)(m0 + r) * (uint32_t)K + 8u * (uint32_t)c) * 2u;
+  }
+  auto xcopy = [&](int kt, uint8_t* st) {
+    const uint32_t so = 128u * (uint32_t)kt;
+#pragma unroll
+    for (int i = 0; i < MI; ++i) lds_copy16(xr, st + 1024 * (MI * wave + i), kt < KT ? xoff[i] : kOOB, so);
+  };
+
+  const int br = tid % QBN, h = tid / QBN;                      // h uniform per wave
+  const uint32_t row = (uint32_t)(n0 + br);
+  const bool row_in = n0 + br < N;
+  const int swb = lds_swz(br);
+  typename W::Raw raw[3];
+  auto rload = [&](int kt, typename W::Raw& slot) { gw_load<W>(g, row, kt, h, row_in && kt < KT, slot, gs); };
+  auto deq = [&](const typename W::Raw& slot, auto chc, int kt, uint8_t* st) {
+    constexpr int CH = decltype(chc)::value;
+    uint32_t o[4];
+    W::template decode<CH>(slot, h, o, kt);
+    *(u32x4*)(st + br * 128 + (((4 * h + CH) ^ swb) << 4)) = u32x4{o[0], o[1], o[2], o[3]};
+  };
+
+  const uint32_t foff0 = (uint32_t)((lane & 31) * 128 + (((lane >> 5) ^ lds_swz(lane & 31)) << 4));
+  const int arow = 32 * MI * wm, brow = 32 * NI * wn;
+  f16x8 af[2][MI], bf[2][NI];
+  auto frag = [&](const uint8_t* xsb, const uint8_t* wsb, int ks, int s) {
+    const uint32_t fo = foff0 ^ ((uint32_t)ks << 5);
+#pragma unroll
+    for (int i = 0; i < MI; ++i) af[s][i] = *(const f16x8*)(xsb + (arow + 32 * i) * 128 + fo);
+#pragma unroll
+    for (int j = 0; j < NI; ++j) bf[s][j] = *(const f16x8*)(wsb + (brow + 32 * j) * 128 + fo);
+  };
+  f32x16 acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // step kt (J = kt % 6): MFMAs on x stage kt%3 and weight stage kt%2; x(kt+2) copied
+  // first; step kt+1's weights (ring slot (kt+1)%3) decoded into weight stage
+  // (kt+1)%2 between the MFMA substeps; step kt+4's bytes loaded into that slot last
+  auto step = [&](auto Jc, int kt) {
+    constexpr int J = decltype(Jc)::value;
+    constexpr int R1 = (J + 1) % 3;
+    const uint8_t* xc = XS[J % 3];
+    const uint8_t* wc = WS[J & 1];
+    xcopy(kt + 2, XS[(J + 2) % 3]);
+    frag(xc, wc, 0, 0);
+    xs_static_for<0, 4>([&](auto ksc) {
+      constexpr int ks = decltype(ksc)::value, cs = ks & 1;
+      if constexpr (ks < 3) frag(xc, wc, ks + 1, cs ^ 1);
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int jn = 0; jn < NI; ++jn)
+          acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cs][i], bf[cs][jn], acc[i][jn], 0, 0, 0);
+      deq(raw[R1], ksc, kt + 1, WS[(J + 1) & 1]);      // chunk ks of step kt+1's weights
+    });
+    __builtin_amdgcn_sched_barrier(0);
+    rload(kt + 4, raw[R1]);
+    // x(kt+1) is done once at most the loads issued after it are outstanding: the
+    // prefetch of step kt-1, x(kt+2) and this prefetch
+    step_barrier<2 * W::NL + MI>();
+  };
+
+  // prologue: steps 0..2 loaded (slots 0..2), x of steps 0 and 1, step 0 decoded into
+  // weight stage 0, step 3 into slot 0
+#pragma unroll
+  for (int p = 0; p < 3; ++p) rload(p, raw[p]);
+  xcopy(0, xs0);
+  xcopy(1, xs1);
+  xs_static_for<0, 4>([&](auto chc) { deq(raw[0], chc, 0, ws0); });
+  __builtin_amdgcn_sched_barrier(0);
+  rload(3, raw[0]);
+  step_barrier<MI + W::NL>();
+  int kt = 0;
+  for (; kt + 6 <= KT; kt += 6) {
+    step(std::integral_constant<int, 0>(), kt + 0);
+    step(std::integral_constant<int, 1>(), kt + 1);
+    step(std::integral_constant<int, 2>(), kt + 2);
+    step(std::integral_constant<int, 3>(), kt + 3);
+    step(std::integral_constant<int, 4>(), kt + 4);
+    step(std::integral_constant<int, 5>(), kt + 5);
+  }
+  // 0..5 more steps
+  if (kt < KT) step(std::integral_constant<int, 0>(), kt + 0);
+  if (kt + 1 < KT) step(std::integral_constant<int, 1>(), kt + 1);
+  if (kt + 2 < KT) step(std::integral_constant<int, 2>(), kt + 2);
+  if (kt + 3 < KT) step(std::integral_constant<int, 3>(), kt + 3);
+  if (kt + 4 < KT) step(std::integral_constant<int, 4>(), kt + 4);
+
+  constexpr uint32_t esz = sizeof(YT);
+  const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)y, (short)0, (int)((uint32_t)M * (uint32_t)N * esz), ALLOY_RSRC_DW3);
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int jn = 0; jn < NI; ++jn) {
+      const int n = n0 + brow + 32 * jn + (lane & 31);
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const int m = m0 + arow + 32 * i + 8 * (t >> 2) + 4 * (lane >> 5) + (t & 3);
+        const uint32_t off = n < N ? ((uint32_t)m * (uint32_t)N + (uint32_t)n) * esz : kOOB;
+        const float v = acc[i][jn][t];
+        if constexpr (sizeof(YT) == 4)
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), yr, off, 0, 0);
+        else
+          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (f16)v), yr, off, 0, 0);
+      }
+    }
+}
+
 // Sum of the S fp32 split-K partial slices, in slice order (deterministic).
 template <typename YT>
 __global__ __launch_bounds__(256) void k_splitk_sum(const float* ws, int S, int64_t mn, YT* y) {
@@ -471,6 +849,54 @@ static hipError_t launch_gemm_q4k(const QArgs& a, const void* x, void* y, bool y
   }
 }
 
+// other formats on the swizzled kernel: tile 256x256, 128x256 or 64x256 by the same
+// last-round fill score as the Q4_K plan (no K split); hipErrorNotSupported when the
+// shape does not fit it (K not a multiple of 64 / 256 for Q6_K, fp32 activations,
+// buffers of 2 GiB or more, MLX group size not a multiple of 32)
+template <class W>
+static hipError_t launch_gemm_w(int fmt, const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32, int64_t M,
+                                int64_t N, const Opts& o, hipStream_t st) {
+  const int64_t K = a.K;
+  if (x_f32 || K % (fmt == F_Q6_K ? 256 : 64) || (fmt == F_MLX && (a.gs < 32 || a.gs % 32)))
+    return hipErrorNotSupported;
+  const uint32_t sb = fmt == F_MLX ? (uint32_t)(2 * (K / a.gs)) : (fmt == F_Q8_0S || fmt == F_Q5_0S) ? (uint32_t)(2 * (K / 32)) : 0u;
+  if ((uint64_t)M * (uint64_t)K * 2u >= (1ull << 31) || (uint64_t)N * (uint64_t)a.rb >= (1ull << 31) ||
+      (uint64_t)N * sb >= (1ull << 31) || (uint64_t)M * (uint64_t)N * 4u >= (1ull << 31))
+    return hipErrorNotSupported;
+  GemmArgs g{a.w, a.aux, a.s, a.b, (uint32_t)N * (uint32_t)a.rb, (uint32_t)N * sb, (uint32_t)a.rb, sb};
+  // forced tile (variants 4, 5, 7 = 256x256, 128x256, 64x256), else the fill score
+  int mi = o.variant == 4 ? 4 : o.variant == 5 ? 2 : o.variant == 7 ? 1 : 0;
+  if (!mi) {
+    const int cus = cu_count();
+    const int bm[3] = {256, 128, 64}, mis[3] = {4, 2, 1};
+    // measured at M = 2048 on the config 3 / 4 shapes (MLX: the 128x256 tile is slower)
+    const double rate[3] = {1000e12, GwR128<W>::value * 1000e12, 0.59 * 1000e12};
+    double best = 1e30;
+    for (int k = GwMaxMi<W>::value >= 4 ? 0 : 1; k < 3; ++k) {
+      const int64_t wg = ((M + bm[k] - 1) / bm[k]) * ((N + 255) / 256), rounds = (wg + cus - 1) / cus;
+      const double t = 1.0 / (rate[k] * (double)wg / (double)(rounds * cus));
+      if (t < best) { best = t; mi = mis[k]; }
+    }
+  }
+  auto go = [&](auto mic) {
+    constexpr int MI = decltype(mic)::value;
+    const dim3 grid((unsigned)((N + 255) / 256), (unsigned)((M + 64 * MI - 1) / (64 * MI)));
+    if (y_f32)
+      hipLaunchKernelGGL((k_gemm_w<W, MI, float>), grid, dim3(512), 0, st, g, (const f16*)x, (int)M, (float*)y, (int)N,
+                         (int)K, a.gs);
+    else
+      hipLaunchKernelGGL((k_gemm_w<W, MI, f16>), grid, dim3(512), 0, st, g, (const f16*)x, (int)M, (f16*)y, (int)N,
+                         (int)K, a.gs);
+    return hipGetLastError();
+  };
+  if (mi > GwMaxMi<W>::value) mi = GwMaxMi<W>::value;
+  if constexpr (GwMaxMi<W>::value >= 4) {
+    if (mi == 4) return go(std::integral_constant<int, 4>());
+  }
+  if (mi == 2) return go(std::integral_constant<int, 2>());
+  return go(std::integral_constant<int, 1>());
+}
+
 template <class F>
 static hipError_t launch_gemm_generic(const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32, int64_t M,
                                       int64_t N, hipStream_t st) {
@@ -487,6 +913,22 @@ hipError_t launch_gemm(int fmt, const QArgs& a, const void* x, bool x_f32, void*
   if (M == 0 || N == 0) return hipSuccess;
   if (fmt == F_Q4_K && !x_f32 && gemm_q4k_fits(M, N, a) && (M > 64 || o.variant >= 4) && o.variant != 1)
     return launch_gemm_q4k(a, x, y, y_f32, M, N, o, ws, ws_bytes, st);
+  // the other formats: the swizzled kernel unless the 128x128 kernel is forced (variant
+  // 1) or the shape does not fit it
+  if (fmt != F_Q4_K && M > 64 && o.variant != 1) {
+    hipError_t e = hipErrorNotSupported;
+    switch (fmt) {
+      case F_Q8_0: e = launch_gemm_w<GWQ80>(fmt, a, x, x_f32, y, y_f32, M, N, o, st); break;
+      case F_Q5_0: e = launch_gemm_w<GWQ50>(fmt, a, x, x_f32, y, y_f32, M, N, o, st); break;
+      case F_Q6_K: e = launch_gemm_w<GWQ6K>(fmt, a, x, x_f32, y, y_f32, M, N, o, st); break;
+      case F_MLX: e = launch_gemm_w<GWMLX>(fmt, a, x, x_f32, y, y_f32, M, N, o, st); break;
+      case F_Q8_0S: e = launch_gemm_w<GWQ80S>(fmt, a, x, x_f32, y, y_f32, M, N, o, st); break;
+      case F_Q5_0S: e = launch_gemm_w<GWQ50S>(fmt, a, x, x_f32, y, y_f32, M, N, o, st); break;
+      default: break;
+    }
+    if (e != hipErrorNotSupported) return e;
+    (void)hipGetLastError();
+  }
   switch (fmt) {
     case F_Q8_0: return launch_gemm_generic<FQ80>(a, x, x_f32, y, y_f32, M, N, st);
     case F_Q5_0: return launch_gemm_generic<FQ50>(a, x, x_f32, y, y_f32, M, N, st);

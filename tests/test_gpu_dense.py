@@ -195,6 +195,33 @@ def test_gemm(dev, fmt, M, N, K):
         for variant in (1, 4, 5, 6, 7, 8):
             yv = wt.qmm(xt, path="gemm", out_dtype=torch.float32, opts=variant << 36)
             check(yv.cpu().numpy(), x, wt.W, f"{fmt} gemm M={M} N={N} K={K} variant={variant}")
+    else:
+        # 1 = 128x128 kernel; 4/5/7 = the swizzled kernel's 256x256 / 128x256 / 64x256 tiles
+        for variant in (1, 4, 5, 7):
+            yv = wt.qmm(xt, path="gemm", out_dtype=torch.float32, opts=variant << 36)
+            check(yv.cpu().numpy(), x, wt.W, f"{fmt} gemm M={M} N={N} K={K} variant={variant}")
+
+
+SWIZZLED_FORMATS = ["q8_0", "q5_0", "q6_k", "mlx_q4", "q8_0_split", "q5_0_split"]
+
+
+@pytest.mark.parametrize("fmt", SWIZZLED_FORMATS)
+@pytest.mark.parametrize("M,N,Ks", [(100, 300, 7), (257, 130, 17), (65, 512, 1), (96, 256, 3)])
+def test_gemm_swizzled_other_formats(dev, fmt, M, N, Ks):
+    """The swizzled GEMM for the other formats: K in 64-element steps (1, 3, 7 and 17
+    steps: prologue only, the unrolled loop's tail and a full unroll plus tail; Q6_K in
+    256-element super-blocks), rows and tokens past the tiles, every tile, fp32 and
+    fp16 outputs; the blocks of the matrix's last row end at the end of its buffer."""
+    K = 64 * Ks if fmt != "q6_k" else 256 * Ks
+    rng = np.random.default_rng(M + N + Ks)
+    wt = Weight(fmt, N, K, rng, dev)
+    x = synth.numpy_x(M, K, rng)
+    xt = torch.from_numpy(x).to(dev)
+    for variant in (0, 4, 5, 7):
+        yv = wt.qmm(xt, path="gemm", out_dtype=torch.float32, opts=variant << 36)
+        check(yv.cpu().numpy(), x, wt.W, f"{fmt} swizzled gemm M={M} N={N} K={K} variant={variant}")
+    y16 = wt.qmm(xt, path="gemm", opts=5 << 36)
+    check(y16.float().cpu().numpy(), x, wt.W, f"{fmt} swizzled gemm fp16 out M={M} N={N} K={K}")
 
 
 @pytest.mark.parametrize("M,N,K", [(130, 200, 768), (300, 130, 2816), (65, 257, 256)])
