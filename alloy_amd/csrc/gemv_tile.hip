@@ -57,7 +57,7 @@ __global__ __launch_bounds__(256) void k_gemv_t(QArgs a, const f16* x, int M, YT
     for (int c = 0; c < kMaxCpl; ++c)
       if (c < cpl) {
         const uint32_t o = (uint32_t)c * 4096u + (uint32_t)t * 16u;
-        v[c] = __builtin_amdgcn_raw_buffer_load_b128(wr, o < tb ? base + o : 0x80000000u, 0, 0);
+        v[c] = __builtin_amdgcn_raw_buffer_load_b128(wr, o < tb ? base + o : 0x80000000u, 0, kStream);
       }
   };
   load_tile(tl);
