@@ -13,10 +13,12 @@ is 7x the 256 MB Infinity Cache, so every launch streams its weights from HBM.
 Prints ONE JSON line.  The step's 197 launches are captured once in a HIP graph (the decode loop is
 launch-bound otherwise); ``value`` = total weight bytes x K / elapsed time of K
 graph replays (HIP events on the replay stream, synchronized on both sides).
-``roofline`` is for the dominant kernel (the Q4_K v_dot2 GEMV): its average
-launch duration per weight shape comes from a graph of launches over distinct weights
-of that shape totalling >= 512 MB (HBM-cold), timed the same way (``--roofline-only``
-runs just these graphs, for the profiler).  ``cpu_baseline`` times the CPU restatement
+``roofline`` is for the dominant kernel (the Q4_K v_dot2 GEMV, every launch of the
+step): algorithmic bytes per launch / the timed region's average launch duration (time
+per step / 197); ``per_shape`` adds each weight shape's average launch duration from a
+graph of launches over distinct weights of that shape totalling >= 512 MB (HBM-cold),
+timed the same way (``--roofline-only`` runs the step and these graphs, for the
+profiler).  ``cpu_baseline`` times the CPU restatement
 (NumPy dequant + PyTorch-CPU fp32 matmul) on one layer and on configs 1, 3, 4 and 5.
 ``prefill_gemm`` reports the Q4_K MFMA GEMM at M = 512, 2048, 4096 on the three config-4
 shapes, ``prefill_gemm_other_formats`` the other formats' GEMM at M = 2048;
@@ -162,17 +164,20 @@ def _median_time(fn, budget_s, max_reps=20, min_reps=3):
     return sorted(times)[len(times) // 2], len(times)
 
 
-def roofline(mats, xs, ys, qmm, dev, total_bytes):
-    """Roofline of the dominant kernel (the Q4_K M=1 GEMV): each weight shape's average
-    launch duration (per_shape_times), weighted by its launches in the step; algorithmic
-    bytes of a launch = its N*K/256*144 weight bytes."""
+def roofline(mats, xs, ys, qmm, dev, total_bytes, step_s):
+    """Roofline of the dominant kernel (the Q4_K M=1 GEMV, every launch of the step):
+    algorithmic bytes per launch = the step's N*K/256*144 weight bytes / its launches;
+    average launch duration = the timed region's time per step (HIP events on the replay
+    stream) / launches.  per_shape: each weight shape's average launch duration from its
+    own graph over >= 512 MB of distinct weights (per_shape_times), and the step fraction
+    those give when weighted by the shapes' launches (per_shape_frac)."""
     per = per_shape_times(mats, xs, ys, qmm, dev)
     counts = {}
     for _, K, N, _ in mats:
         counts[(K, N)] = counts.get((K, N), 0) + 1
     tot_t = sum(per[k] * c for k, c in counts.items())
-    achieved = total_bytes / tot_t / 1e9
     launches = len(mats)
+    achieved = total_bytes / step_s / 1e9
     shapes = {f"{K}x{N}": {"us": round(v * 1e6, 2), "GBps": round(q4k_bytes(K, N) / v / 1e9, 1),
                            "launches_per_step": counts[(K, N)]}
               for (K, N), v in per.items()}
@@ -180,7 +185,9 @@ def roofline(mats, xs, ys, qmm, dev, total_bytes):
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
             "kernel": "k_gemv_w<FQ4K> (Q4_K M=1 wave-row GEMV)",
             "bytes_per_launch": round(total_bytes / launches),
-            "avg_launch_us": round(tot_t / launches * 1e6, 3), "per_shape": shapes}
+            "avg_launch_us": round(step_s / launches * 1e6, 3), "per_shape": shapes,
+            "per_shape_frac": round(total_bytes / tot_t / 1e9 / HBM_PEAK_GBS, 4),
+            "per_shape_avg_launch_us": round(tot_t / launches * 1e6, 3)}
 
 
 def cpu_baseline():
@@ -503,7 +510,10 @@ def main():
     mats, xs, ys = build_decode_step(dev)
     total_bytes = sum(q4k_bytes(K, N) for _, K, N, _ in mats)
     if args.roofline_only:
-        print(json.dumps({"roofline": roofline(mats, xs, ys, qmm, dev, total_bytes)}))
+        g = capture(lambda: run_step(mats, xs, ys, qmm), dev)
+        t = time_replays(g, args.steps, args.warmup, torch.cuda.current_stream(dev))
+        del g
+        print(json.dumps({"roofline": roofline(mats, xs, ys, qmm, dev, total_bytes, t / args.steps)}))
         return
     stream = torch.cuda.current_stream(dev)
     if args.eager:
@@ -538,7 +548,7 @@ def main():
                        "(one launch serving several matrices), fp16 outputs"}
     log(json.dumps({"batched_step": batched}))
 
-    roof = roofline(mats, xs, ys, qmm, dev, total_bytes)
+    roof = roofline(mats, xs, ys, qmm, dev, total_bytes, t / args.steps)
     log(json.dumps(roof["per_shape"]))
 
     prefill = None if args.no_prefill else prefill_gemm(dev, qmm)
