@@ -100,7 +100,8 @@ const char* alloy_last_error(void) { return g_err.c_str(); }
 const char* alloy_version(void) { return "alloy_amd 0.1.0 (gfx950)"; }
 
 int64_t alloy_gemm_workspace_bytes(alloy_format fmt, int64_t M, int64_t N, int64_t K) {
-  if (M <= 16 || M > 65535LL * 128 || N <= 0 || K <= 0) return 0;
+  if (M < 2 || M > 65535LL * 128 || N <= 0 || K <= 0) return 0;
+  if (M <= 16) return alloy::gemv_workspace_bytes((int)fmt, M, N, K);
   return alloy::gemm_workspace_bytes((int)fmt, M, N, K);
 }
 
@@ -147,7 +148,8 @@ alloy_status alloy_qmm_ws(alloy_format fmt, const void* w, const void* aux, cons
       return hip_status(alloy::launch_gemv_dot2((int)fmt, a, x, xf, y, yf, M, N, o, st), "gemv_dot2 launch");
     case alloy::P_GEMV_MFMA:
       if (M > 65535 * 16) return fail(ALLOY_E_SHAPE, "MFMA GEMV: M=%lld too large", (long long)M);
-      return hip_status(alloy::launch_gemv_mfma((int)fmt, a, x, xf, y, yf, M, N, o, st), "gemv_mfma launch");
+      if (ws_bytes < 0 || (ws_bytes > 0 && !ws)) return fail(ALLOY_E_ARG, "bad workspace (%lld bytes)", (long long)ws_bytes);
+      return hip_status(alloy::launch_gemv_mfma((int)fmt, a, x, xf, y, yf, M, N, o, st, ws, ws_bytes), "gemv_mfma launch");
     case alloy::P_GEMM:
       if (M > 65535LL * 128) return fail(ALLOY_E_SHAPE, "GEMM: M=%lld too large", (long long)M);
       if (ws_bytes < 0 || (ws_bytes > 0 && !ws)) return fail(ALLOY_E_ARG, "bad workspace (%lld bytes)", (long long)ws_bytes);

@@ -1123,8 +1123,14 @@ struct GemvMfmaRun {
 // M <= 16 on the generic x-stationary kernel (Q4_K, Q6_K, MLX with a power-of-two
 // group size; GGUF wire Q5_0 / Q8_0 with dequantised weights only); hipErrorNotSupported
 // when the format or shape does not fit it.
+static hipError_t launch_xs_job(int fmt, XsJob j, const Opts& o, hipStream_t st, bool dq);
+
+// splits > 1 (with ws holding splits M N fp32): K cut into that many ranges of whole
+// 256-element units, one grid row of workgroups each writing its fp32 partial slice,
+// then the slices summed in order into y (deterministic)
 static hipError_t launch_gemv_xs(int fmt, const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32,
-                                 int64_t M, int64_t N, const Opts& o, hipStream_t st, bool dq = false) {
+                                 int64_t M, int64_t N, const Opts& o, hipStream_t st, bool dq = false,
+                                 int splits = 1, float* ws = nullptr) {
   if (x_f32 || M > 16 || N >= (1ll << 31) || (uint64_t)M * (uint64_t)a.K * 2u >= (1ull << 31))
     return hipErrorNotSupported;
   XsJob j{};
@@ -1136,6 +1142,25 @@ static hipError_t launch_gemv_xs(int fmt, const QArgs& a, const void* x, bool x_
   j.N = (int)N;
   j.y = y;
   j.y_f32 = y_f32;
+  const int KU = a.K / 256;
+  if (splits > 1 && ws && a.K % 256 == 0 && KU >= 2) {
+    const int ku = (KU + splits - 1) / splits;
+    const int S = (KU + ku - 1) / ku;
+    if (S > 1) {
+      j.ku_split = ku;
+      j.y = ws;
+      j.y_f32 = 1;
+      const hipError_t e = launch_xs_job(fmt, j, o, st, dq);
+      if (e != hipSuccess) return e;
+      return launch_splitk_sum(ws, S, M * N, y, y_f32, st);
+    }
+  }
+  return launch_xs_job(fmt, j, o, st, dq);
+}
+
+static hipError_t launch_xs_job(int fmt, XsJob j, const Opts& o, hipStream_t st, bool dq) {
+  const QArgs& a = j.a;
+  const int64_t M = j.M, N = j.N;
   const int64_t cap = o.grid_cap > 0 ? o.grid_cap : 1024;
   if (dq) {
     // measured on the config 2 / 3 shapes: wide matrices loop one workgroup per CU
@@ -1235,9 +1260,35 @@ static int mfma_variant(int fmt, int64_t M, int64_t N, int64_t K) {
   return 1;
 }
 
+// K splits of the x-stationary kernels (1: none).  Measured at M = 8 / 16 (graph
+// replays): with few 16-row tiles the grid leaves most CUs idle and each workgroup's
+// chain grows with K; four splits at <= 64 tiles (Q6_K M = 8 14336x1024 30.0 -> 11.5 us,
+// 4096x1024 8.9 -> 7.2 us; Q5_0 / Q8_0 / MLX / Q4_K alike), two at <= 128 (M = 16
+// 4096x2048 10.7 -> 9.5 us); at 192 tiles and more splits lose (extra partial traffic
+// and the summing launch).  K >= 4096 keeps at least four units per split; Q4_K over
+// K = 8192 takes the Q4_K x-stationary kernel, which does not split.
+static int gemv_splits(int fmt, int64_t M, int64_t N, int64_t K) {
+  if (M < 8 || M > 16 || K < 4096 || K % 256 || (fmt == F_Q4_K && K > 8192)) return 1;
+  if (fmt != F_Q4_K && fmt != F_Q6_K && fmt != F_Q5_0 && fmt != F_Q8_0 && fmt != F_MLX) return 1;
+  const int64_t tiles = (N + 15) / 16;
+  return tiles <= 64 ? 4 : tiles <= 128 ? 2 : 1;
+}
+
+int64_t gemv_workspace_bytes(int fmt, int64_t M, int64_t N, int64_t K) {
+  if (M < 2 || M > 16 || N <= 0 || K <= 0) return 0;
+  const int S = gemv_splits(fmt, M, N, K);
+  return S > 1 ? (int64_t)S * M * N * 4 : 0;
+}
+
 hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
-                            bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st) {
+                            bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st,
+                            void* ws, int64_t ws_bytes) {
   if (M == 0 || N == 0) return hipSuccess;
+  // K splits: forced (opts) or planned, when the workspace holds the partials
+  int splits = o.splits > 1 ? o.splits : gemv_splits(fmt, M, N, a.K);
+  if (splits > 1 && (!ws || ws_bytes < (int64_t)splits * M * N * 4 || (M * N) % 4 || ((uintptr_t)ws & 15) ||
+                     ((uintptr_t)y & (y_f32 ? 15 : 7))))
+    splits = 1;
   // few activation rows on few rows: the LDS-staged v_dot2 kernel (weights read once,
   // decoded once per row and token) beats the MFMA kernels' fixed cost — measured on
   // the BASELINE decode shapes at M = 2, 3, 4, 8
@@ -1246,8 +1297,8 @@ hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, 
   const int v = o.variant ? o.variant : tile_small_m ? 9 : mfma_variant(fmt, M, N, a.K);
   hipError_t e = hipErrorNotSupported;
   if (v == 9) e = launch_gemv_tile(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
-  else if (v == 7) e = launch_gemv_xs(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
-  else if (v == 8) e = launch_gemv_xs(fmt, a, x, x_f32, y, y_f32, M, N, o, st, true);
+  else if (v == 7) e = launch_gemv_xs(fmt, a, x, x_f32, y, y_f32, M, N, o, st, false, splits, (float*)ws);
+  else if (v == 8) e = launch_gemv_xs(fmt, a, x, x_f32, y, y_f32, M, N, o, st, true, splits, (float*)ws);
   else if (v == 6 && fmt == F_Q4_K) e = launch_gemv_xs_q4k(a, x, x_f32, y, y_f32, M, N, o, st);
   else if (v == 5 && fmt == F_Q4_K) e = launch_gemv_q4k_m4(a, x, x_f32, y, y_f32, M, N, o, st);
   if (e != hipErrorNotSupported) return e;

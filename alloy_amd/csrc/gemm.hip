@@ -767,6 +767,14 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float* ws, int S, int6
   }
 }
 
+hipError_t launch_splitk_sum(const float* ws, int S, int64_t mn, void* y, bool y_f32, hipStream_t st) {
+  if (mn % 4 || ((uintptr_t)ws & 15) || ((uintptr_t)y & (y_f32 ? 15 : 7))) return hipErrorNotSupported;
+  const int64_t blocks = (mn / 4 + 255) / 256;
+  if (y_f32) hipLaunchKernelGGL(k_splitk_sum<float>, dim3((unsigned)blocks), dim3(256), 0, st, ws, S, mn, (float*)y);
+  else hipLaunchKernelGGL(k_splitk_sum<f16>, dim3((unsigned)blocks), dim3(256), 0, st, ws, S, mn, (f16*)y);
+  return hipGetLastError();
+}
+
 // Q4_K GEMM plan: tile kind (0 = 256x256, 1 = 128x256, 2 = 128x128, 3 = 64x256,
 // 4 = 64x128) and K splits S.  Each kind's measured full-chip rate (TFLOP/s on
 // MI355X) is scaled by the fraction of CU slots its tile count x S fills in the last

@@ -56,8 +56,16 @@ hipError_t launch_gemv_tile(int fmt, const QArgs& a, const void* x, bool x_f32, 
                             int64_t N, const Opts& o, hipStream_t st);
 hipError_t launch_gemv_dot2(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
                             bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st);
+// 2 <= M <= 16.  ws (ws_bytes): optional fp32 workspace for a K-split plan,
+// gemv_workspace_bytes() of it (0: no split); without it the plan has no split.
 hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, void* y,
-                            bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st);
+                            bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st,
+                            void* ws = nullptr, int64_t ws_bytes = 0);
+int64_t gemv_workspace_bytes(int fmt, int64_t M, int64_t N, int64_t K);
+// y (M x N, mn = M N, a multiple of 4) = the sum of the S fp32 slices ws[s][mn] in
+// slice order; ws 16-byte and y 16- (fp32) or 8-byte (fp16) aligned, else
+// hipErrorNotSupported.
+hipError_t launch_splitk_sum(const float* ws, int S, int64_t mn, void* y, bool y_f32, hipStream_t st);
 // Prefill GEMM.  ws (ws_bytes): optional fp32 workspace for the Q4_K split-K plan,
 // gemm_workspace_bytes() of it (0: no split); without it the plan has no split.
 hipError_t launch_gemm(int fmt, const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32,

@@ -616,6 +616,9 @@ struct XsJob {
   float* part;             // MODE 2 output
   int W;                   // waves per workgroup (set by the launcher)
   int kp;                  // K passes (multi-pass kernel; set by the launcher)
+  int ku_split;            // MODE 0: 256-element units per K split (grid.y = split s
+                           // takes units [s ku_split, (s + 1) ku_split) and writes fp32
+                           // partials to y + s M N); 0: no split
 };
 
 // a * b rounded to fp32.  The empty asm (no instruction) pins the fp32 value: without
@@ -668,11 +671,21 @@ __global__ __launch_bounds__(MP ? 64 * XsMPW<P>::value : 1024) void k_gemv_xs(Xs
   float* tmx = red + W * RT * 64 * 4 * NM;               // [W][16] token |x| maxima (MODE 2)
   float* tsc = tmx + W * 16;                             // [16] token scales (MODE 2)
   const int n16 = lane & 15, kq = lane >> 4;
-  int u0 = wave * UPW;                                   // first unit of this wave (this pass)
-  int nu = KU - u0 < UPW ? KU - u0 : UPW;                // units present (uniform; <= 0: none)
+  // this workgroup's units [ubase, uend): all of K, or its K split (MODE 0)
+  int ubase = 0, uend = KU;
+  int64_t yoff = 0;                                      // its output slice (K split: partials)
+  if constexpr (MODE == 0) {
+    if (j.ku_split > 0) {
+      ubase = (int)blockIdx.y * j.ku_split;
+      uend = KU - ubase < j.ku_split ? KU : ubase + j.ku_split;
+      yoff = (int64_t)blockIdx.y * j.M * j.N;
+    }
+  }
+  int u0 = ubase + wave * UPW;                           // first unit of this wave (this pass)
+  int nu = uend - u0 < UPW ? uend - u0 : UPW;            // units present (uniform; <= 0: none)
   auto set_pass = [&](int p) {
-    u0 = (p * W + wave) * UPW;
-    nu = KU - u0 < UPW ? KU - u0 : UPW;
+    u0 = ubase + (p * W + wave) * UPW;
+    nu = uend - u0 < UPW ? uend - u0 : UPW;
   };
 
   int cnt = j.M, p0 = 0, tok = 0;
@@ -835,7 +848,7 @@ __global__ __launch_bounds__(MP ? 64 * XsMPW<P>::value : 1024) void k_gemv_xs(Xs
         if constexpr (NM == 2) v1 += q[4 + tt];
       }
       if constexpr (MODE == 0) {
-        ((YT*)j.y)[(int64_t)tk * j.N + n] = (YT)v0;
+        ((YT*)j.y)[yoff + (int64_t)tk * j.N + n] = (YT)v0;
       } else if constexpr (MODE == 3) {
         ((YT*)j.y)[(int64_t)tk * j.N + n] = (YT)xs_f32_product(xs_act(j.act, v0), v1);
       } else if constexpr (MODE == 1) {
@@ -980,10 +993,14 @@ hipError_t launch_xs(const XsJob& j, int64_t tiles_y, int64_t cap, int rt, hipSt
   constexpr bool DENSE = MODE == 0 || MODE == 3;
   const int K = j.a.K;
   if (K <= 0 || K % 256 || j.M > 16 || j.N <= 0) return hipErrorNotSupported;
+  // K split (MODE 0): the plan below is that of one split's K
+  const int KU = K / 256;
+  const int ksplit = MODE == 0 && j.ku_split > 0 && j.ku_split < KU ? j.ku_split : 0;
+  const int splits = ksplit ? (KU + ksplit - 1) / ksplit : 1;
   const uint64_t rows = (uint64_t)j.N + 16u;
   if (rows * (uint64_t)j.a.rb >= (1ull << 31) || rows * j.sb >= (1ull << 31) || j.xbytes >= (1u << 31))
     return hipErrorNotSupported;
-  const int KS = K / 32;
+  const int KS = (ksplit ? ksplit * 256 : K) / 32;
   int ns = KS <= 8 * 16 ? 8 : KS <= 16 * 16 ? 16 : 0;   // at most 16 waves
   int kp = 1;
   if (ns != 8 && MODE == 0 && XsIsDQ<P>::value && !P::WIDE) {
@@ -1012,20 +1029,22 @@ hipError_t launch_xs(const XsJob& j, int64_t tiles_y, int64_t cap, int rt, hipSt
     }
     int64_t gx = groups;
     if (pipe) {
-      const int64_t c = cap > 0 ? cap : (int64_t)resident_per_cu((const void*)kern, 64 * W, lds) * cu_count();
+      int64_t c = cap > 0 ? cap : (int64_t)resident_per_cu((const void*)kern, 64 * W, lds) * cu_count();
+      c = c / splits > 0 ? c / splits : 1;              // the K splits share the resident slots
       gx = groups < c ? groups : c;
     }
-    const dim3 grid((unsigned)gx, DENSE ? 1u : (unsigned)tiles_y), block((unsigned)(64 * W));
+    const dim3 grid((unsigned)gx, DENSE ? (unsigned)splits : (unsigned)tiles_y), block((unsigned)(64 * W));
     XsJob jw = j;
     jw.W = W;
     jw.kp = kp;
+    jw.ku_split = ksplit;
     hipLaunchKernelGGL(kern, grid, block, lds, st, jw);
     return hipGetLastError();
   };
   // whether the tiles outnumber the resident workgroups of the one-pass kernel
   auto many = [&](auto kern) -> bool {
     const int64_t c = cap > 0 ? cap : (int64_t)resident_per_cu((const void*)kern, 64 * W, lds) * cu_count();
-    return groups > c;
+    return groups * splits > c;
   };
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;

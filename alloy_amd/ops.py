@@ -131,7 +131,7 @@ def qmm(fmt: str, x: torch.Tensor, w: torch.Tensor, *, scales=None, biases=None,
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=dev)
     with torch.cuda.device(dev):
-        ws = gemm_workspace(fmt, M, N, K, dev, opts) if path in ("auto", "gemm") else None
+        ws = gemm_workspace(fmt, M, N, K, dev, opts) if path in ("auto", "gemm", "gemv_mfma") else None
         _lib.call("alloy_qmm_ws", _lib.FMT[fmt], _p(w), _p(aux), _p(scales), _p(biases), group_size,
                   _p(x), _dt(x.dtype, "activations"), _p(out), _dt(out.dtype, "output"), M, N, K,
                   _lib.PATH[path], opts, _p(ws), 0 if ws is None else ws.numel(), _stream(dev))
@@ -139,11 +139,13 @@ def qmm(fmt: str, x: torch.Tensor, w: torch.Tensor, *, scales=None, biases=None,
 
 
 def gemm_workspace(fmt: str, M: int, N: int, K: int, dev, opts: int = 0) -> torch.Tensor | None:
-    """The split-K workspace the prefill GEMM plan wants for this shape (None: no split);
-    with a forced tile and split count in ``opts`` (bits 36-39, 40-43), that split's."""
-    need = int(_lib.lib().alloy_gemm_workspace_bytes(_lib.FMT[fmt], M, N, K)) if M > 16 else 0
-    if (opts >> 36) & 0xF >= 4 and (opts >> 40) & 0xF > 1:
-        need = max(need, ((opts >> 40) & 0xF) * M * N * 4)
+    """The split-K workspace the plan wants for this shape (None: no split): the prefill
+    GEMM's (M > 16) or the M <= 16 kernels'; with a split count forced in ``opts`` (bits
+    40-43; for the GEMM with a forced tile, bits 36-39), that split's."""
+    need = int(_lib.lib().alloy_gemm_workspace_bytes(_lib.FMT[fmt], M, N, K)) if M > 1 else 0
+    forced = (opts >> 40) & 0xF
+    if forced > 1 and (M <= 16 or (opts >> 36) & 0xF >= 4):
+        need = max(need, forced * M * N * 4)
     return torch.empty(need, dtype=torch.uint8, device=dev) if need > 0 else None
 
 

@@ -101,13 +101,15 @@ alloy_status alloy_qmm(alloy_format fmt, const void* w, const void* aux, const v
                        alloy_path path, int64_t opts, void* stream);
 
 /*
- * alloy_qmm with a caller workspace for the prefill GEMM: when the Q4_K GEMM would
- * leave CUs idle (few output tiles, e.g. M = 512), it splits K into S slices whose
- * fp32 partial products go to ws (S*M*N*4 bytes, 16-byte aligned, y 16-byte
- * aligned) and are summed in slice order (deterministic).  ws = NULL or too small:
- * no split.  alloy_gemm_workspace_bytes() returns the bytes the plan wants for this
- * shape (0 when it does not split).  No reference counterpart (the reference has no
- * K split); for callers of the GEMM path that can provide scratch memory.
+ * alloy_qmm with a caller workspace: when the Q4_K prefill GEMM would leave CUs idle
+ * (few output tiles, e.g. M = 512), or an M <= 16 product on the x-stationary kernels
+ * has few row tiles over a long K, K is split into S slices whose fp32 partial
+ * products go to ws (S*M*N*4 bytes, 16-byte aligned; y 16-byte aligned for fp32
+ * output, 8-byte for fp16; M*N a multiple of 4) and are summed in slice order
+ * (deterministic).  ws = NULL or too small: no split.  alloy_gemm_workspace_bytes()
+ * returns the bytes the plan wants for this shape (0 when it does not split).  No
+ * reference counterpart (the reference has no K split); for callers that can
+ * provide scratch memory.
  */
 int64_t alloy_gemm_workspace_bytes(alloy_format fmt, int64_t M, int64_t N, int64_t K);
 alloy_status alloy_qmm_ws(alloy_format fmt, const void* w, const void* aux, const void* scales,

@@ -180,6 +180,29 @@ def test_gemv_xs_multipass(dev, fmt, M, K, N):
     check(y16, x, wt.W, f"{fmt} xs multi-pass fp16 out M={M} K={K} N={N}")
 
 
+@pytest.mark.parametrize("fmt", ["q4_k", "q6_k", "q5_0", "q8_0", "mlx_q4"])
+@pytest.mark.parametrize("M", [3, 8, 16])
+@pytest.mark.parametrize("K,N,splits", [(2048, 132, 3), (8192, 72, 2), (8192, 72, 5), (11008, 40, 4),
+                                        (1024, 40, 7), (2048, 130, 2)])
+def test_gemv_xs_k_split(dev, fmt, M, K, N, splits):
+    """M <= 16 with K cut into ranges of whole 256-element units (one grid row each,
+    fp32 partials summed in order): even splits, a short last split (8192 / 5 = 7 units
+    x 4 + 4, 11008 / 4 = 11 x 3 + 10), more splits than units per wave (1024 / 7 gives
+    4 splits of one unit), multi-pass K inside a split (Q6_K / Q5_0 / Q8_0 at 11008 / 4);
+    M N not a multiple of 4 (M = 3, N = 130) runs unsplit.  fp32 and fp16 output."""
+    if fmt == "q4_k" and K > 8192:
+        pytest.skip("Q4_K over K = 8192 takes the Q4_K x-stationary kernel (no K split)")
+    rng = np.random.default_rng(K + N + M + splits)
+    wt = Weight(fmt, N, K, rng, dev)
+    x = synth.numpy_x(M, K, rng)
+    xt = torch.from_numpy(x).to(dev)
+    opts = splits << 40
+    y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=opts).cpu().numpy()
+    check(y, x, wt.W, f"{fmt} K split M={M} K={K} N={N} S={splits}")
+    y16 = wt.qmm(xt, path="gemv_mfma", opts=opts).float().cpu().numpy()
+    check(y16, x, wt.W, f"{fmt} K split fp16 out M={M} K={K} N={N} S={splits}")
+
+
 @pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("M,N,K", [(33, 130, 1024), (200, 256, 2048), (128, 64, 4096)])
 def test_gemm(dev, fmt, M, N, K):

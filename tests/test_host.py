@@ -65,6 +65,22 @@ def test_moe_workspace_layout():
     assert lib.alloy_moe_workspace_bytes(0, 0, 8, 2048, 768) == 0
 
 
+def test_split_workspace_plan():
+    """The K-split workspace the M <= 16 plan asks for: four fp32 partial slices with
+    <= 64 row tiles, two with <= 128, none beyond, for M < 8, K < 4096 or Q4_K past
+    K = 8192; M = 1 never splits."""
+    lib = alloy_amd.lib()
+    F = _lib.FMT
+    assert lib.alloy_gemm_workspace_bytes(F["q6_k"], 8, 1024, 4096) == 4 * 8 * 1024 * 4
+    assert lib.alloy_gemm_workspace_bytes(F["q5_0"], 16, 2048, 14336) == 2 * 16 * 2048 * 4
+    assert lib.alloy_gemm_workspace_bytes(F["mlx_q4"], 8, 1000, 4096) == 4 * 8 * 1000 * 4
+    assert lib.alloy_gemm_workspace_bytes(F["q8_0"], 8, 4096, 4096) == 0
+    assert lib.alloy_gemm_workspace_bytes(F["q6_k"], 4, 1024, 4096) == 0
+    assert lib.alloy_gemm_workspace_bytes(F["q6_k"], 8, 1024, 3072) == 0
+    assert lib.alloy_gemm_workspace_bytes(F["q4_k"], 16, 1024, 11008) == 0
+    assert lib.alloy_gemm_workspace_bytes(F["q4_k"], 1, 1024, 4096) == 0
+
+
 def meta(shape, dtype):
     return torch.empty(shape, dtype=dtype, device="meta")
 
