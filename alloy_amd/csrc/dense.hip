@@ -275,96 +275,6 @@ __global__ __launch_bounds__(256) void k_gemv_w(WaveBatchT<NB> bt, uint32_t sb, 
   }
 }
 
-// ------------------------------------------------------------------ M=1 GEMV, LDS-staged
-// For the GGUF wire formats (one contiguous blob, 16-byte-multiple rows).  A tile of
-// R whole rows is a contiguous byte range; the workgroup streams it with perfectly
-// coalesced 16-byte loads (every wave instruction reads 1 KB contiguous), keeps two
-// tiles in flight in registers, and double-buffers the tiles in LDS.  Threads then
-// decode their units from LDS exactly as the register-ring kernel does from global
-// memory.  Per tile: one barrier.  Row partial sums of tile i are written to LDS and
-// finalised (fixed order) after the next barrier, so the reduction needs no barrier
-// of its own.
-template <class F, int UPT, int CPW, typename XT>
-__global__ __launch_bounds__(256) void k_gemv_lds(QArgs a, const XT* x, void* y, int y_f32,
-                                                  int64_t N, int C16) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  constexpr int TB = CPW * 4096;                 // bytes per tile buffer
-  float* red = (float*)(lds + 2 * TB);           // [2][16] partial sums
-  const int L = 16 * C16, R = 16 / C16;
-  const int K = a.K, U = K / F::UE;
-  const int t = threadIdx.x, slot = t / L, li = t - slot * L;
-  const bool act = slot < R;
-  const int64_t m = blockIdx.y;
-  const int64_t RB = a.rb, tile_bytes = (int64_t)R * RB, total = N * RB;
-  const int64_t ntiles = (N + R - 1) / R, G = gridDim.x;
-  const int64_t nt = (ntiles - (int64_t)blockIdx.x + G - 1) / G;   // tiles of this workgroup
-  bool own[UPT];
-  int uu[UPT];
-#pragma unroll
-  for (int j = 0; j < UPT; ++j) {
-    own[j] = act && li + L * j < U;
-    uu[j] = (li + L * j < U) ? li + L * j : U - 1;
-  }
-  auto gload = [&](int64_t i, u32x4 (&r)[CPW]) {
-    const int64_t q = (int64_t)blockIdx.x + (i < nt ? i : nt - 1) * G;
-#pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-      int64_t off = q * tile_bytes + 16 * (t + 256 * c);
-      off = off < total - 16 ? off : total - 16;
-      r[c] = __builtin_nontemporal_load((const u32x4*)(a.w + off));
-    }
-  };
-  auto lstore = [&](const u32x4 (&r)[CPW], int b) {
-#pragma unroll
-    for (int c = 0; c < CPW; ++c) *(u32x4*)(lds + b * TB + 16 * (t + 256 * c)) = r[c];
-  };
-  u32x4 r0[CPW], r1[CPW];
-  gload(0, r0);
-  gload(1, r1);
-  uint32_t xr[UPT][F::UE / 2];
-  float xg[UPT][F::UE / 16];
-  const XT* xm = x + m * K;
-#pragma unroll
-  for (int j = 0; j < UPT; ++j) load_x_unit<F, XT>(xm, uu[j], xr[j], xg[j]);
-  lstore(r0, 0);
-  gload(2, r0);
-
-  // row n's sum: partials of its C16 lane groups in red[par][slot*C16 + g]
-  auto finalize = [&](int64_t i, int par) {
-    const int64_t n = ((int64_t)blockIdx.x + i * G) * R + slot;
-    float s = 0.f;
-    for (int g = 0; g < C16; ++g) s += red[par * 16 + slot * C16 + g];
-    if (act && (li & 15) == 0 && n < N) store_y(y, y_f32, m * N + n, s);
-  };
-  auto compute = [&](int64_t i, int b, int par) {
-    const uint8_t* row = lds + b * TB + slot * RB;
-    float acc = 0.f;
-#pragma unroll
-    for (int j = 0; j < UPT; ++j) {
-      const float v = F::dot(F::load_row(row, uu[j]), uu[j], xr[j], xg[j]);
-      acc += own[j] ? v : 0.f;
-    }
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    if (act && (li & 15) == 0) red[par * 16 + slot * C16 + (li >> 4)] = acc;
-  };
-  for (int64_t i = 0; i < nt; i += 2) {
-    __syncthreads();
-    if (i > 0) finalize(i - 1, 1);
-    compute(i, 0, 0);
-    lstore(r1, 1);
-    gload(i + 3, r1);
-    if (i + 1 >= nt) break;
-    __syncthreads();
-    finalize(i, 0);
-    compute(i + 1, 1, 1);
-    lstore(r0, 0);
-    gload(i + 4, r0);
-  }
-  __syncthreads();
-  finalize(nt - 1, (int)((nt - 1) & 1));
-}
-
 // ------------------------------------------------------------------ M<=16 GEMV on MFMA
 // v_mfma_f32_16x16x32_f16 with A = 16 weight rows (dequantised to fp16 in registers),
 // B = x^T (up to 16 activation rows).  A K-chunk of 128 elements is split over the
@@ -689,29 +599,6 @@ struct GemvDot2Run {
       hipLaunchKernelGGL((k_gemv_dot2<F, UPT, 3, XT>), g, b, 0, st, a, (const XT*)x, y, (int)y_f32, N, C16);
     return hipGetLastError();
   }
-  template <int UPT, int CPW, typename XT, class FF = F>
-  static hipError_t go_lds(const QArgs& a, const void* x, void* y, bool y_f32, int64_t M, int64_t N,
-                           int C16, int grid_cap, hipStream_t st) {
-    const int R = 16 / C16;
-    const int64_t ntiles = (N + R - 1) / R;
-    int64_t grid = ntiles;
-    const int64_t cap = grid_cap > 0 ? grid_cap : 1024;
-    if (grid > cap) grid = cap;
-    const size_t shm = 2 * (size_t)CPW * 4096 + 2 * 16 * sizeof(float);
-    hipLaunchKernelGGL((k_gemv_lds<F, UPT, CPW, XT>), dim3((unsigned)grid, (unsigned)M), dim3(256), shm, st,
-                       a, (const XT*)x, y, (int)y_f32, N, C16);
-    return hipGetLastError();
-  }
-  template <int UPT, typename XT>
-  static hipError_t pick_lds(int cpw, const QArgs& a, const void* x, void* y, bool y_f32, int64_t M,
-                             int64_t N, int C16, int cap, hipStream_t st) {
-    switch (cpw) {
-      case 1: return go_lds<UPT, 1, XT>(a, x, y, y_f32, M, N, C16, cap, st);
-      case 2: return go_lds<UPT, 2, XT>(a, x, y, y_f32, M, N, C16, cap, st);
-      case 3: return go_lds<UPT, 3, XT>(a, x, y, y_f32, M, N, C16, cap, st);
-      default: return go_lds<UPT, 4, XT>(a, x, y, y_f32, M, N, C16, cap, st);
-    }
-  }
   static hipError_t run(const QArgs& a, const void* x, bool x_f32, void* y, bool y_f32, int64_t M,
                         int64_t N, const Opts& o, hipStream_t st) {
     const int U = a.K / F::UE;
@@ -721,19 +608,6 @@ struct GemvDot2Run {
     if (o.lanes_per_row >= 16) {                     // explicit override (tuning / tests)
       const int c = o.lanes_per_row / 16;
       if (c * 16 * 2 >= U) { C16 = c > 16 ? 16 : c; upt = C16 * 16 >= U ? 1 : 2; }
-    }
-    const int R = 16 / C16;
-    const int64_t tile = (int64_t)R * a.rb;
-    const int cpw = (int)((tile + 4095) / 4096);
-    // the LDS-staged variant is opt-in: the register ring is faster on every measured shape
-    const bool lds_ok = F::kStaged && a.rb % 16 == 0 && cpw <= 4 && o.variant == 2;
-    if constexpr (F::kStaged) {
-      if (lds_ok) {
-        if (upt == 2) return x_f32 ? pick_lds<2, float>(cpw, a, x, y, y_f32, M, N, C16, o.grid_cap, st)
-                                   : pick_lds<2, f16>(cpw, a, x, y, y_f32, M, N, C16, o.grid_cap, st);
-        return x_f32 ? pick_lds<1, float>(cpw, a, x, y, y_f32, M, N, C16, o.grid_cap, st)
-                     : pick_lds<1, f16>(cpw, a, x, y, y_f32, M, N, C16, o.grid_cap, st);
-      }
     }
     if (upt == 2) return x_f32 ? go<2, float>(a, x, y, y_f32, M, N, C16, o.grid_cap, o.depth, st)
                                : go<2, f16>(a, x, y, y_f32, M, N, C16, o.grid_cap, o.depth, st);

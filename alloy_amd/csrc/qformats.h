@@ -192,7 +192,6 @@ struct Q4kSel {
 
 struct FQ4K {
   static constexpr int QK = 256, BB = 144, UE = 32, XPERM = 4;
-  static constexpr bool kStaged = true;   // rows live in one blob (LDS-staged GEMV)
 
   __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
     const uint8_t* blk = a.w + n * a.rb + (int64_t)(k0 >> 8) * BB;
@@ -323,7 +322,6 @@ struct FQ4K {
 struct FQ6K {
   static constexpr int QK = 256, BB = 210, UE = 64, XPERM = 4;
   static constexpr int RUN = 32;        // x run length (elements) of a unit
-  static constexpr bool kStaged = true;   // rows live in one blob (LDS-staged GEMV)
 
   __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
     const uint8_t* blk = a.w + n * a.rb + (int64_t)(k0 >> 8) * BB;
@@ -418,7 +416,6 @@ __device__ __forceinline__ float q8_words_dot(const uint32_t (&v)[8], const uint
 struct FQ80 {
   static constexpr int QK = 32, BB = 34, UE = 32, XPERM = 4;
   static constexpr int RUN = 32;        // x run length (elements) of a unit
-  static constexpr bool kStaged = true;   // rows live in one blob (LDS-staged GEMV)
 
   __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
     const uint8_t* blk = a.w + n * a.rb + (int64_t)(k0 >> 5) * BB;
@@ -459,7 +456,6 @@ struct FQ80 {
 struct FQ80S {
   static constexpr int QK = 32, BB = 32, UE = 32, XPERM = 4;
   static constexpr int RUN = 32;        // x run length (elements) of a unit
-  static constexpr bool kStaged = false;   // rows live in one blob (LDS-staged GEMV)
 
   __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
     const uint8_t* q = a.w + n * a.rb + k0;
@@ -497,7 +493,6 @@ struct FQ80S {
 struct FQ50 {
   static constexpr int QK = 32, BB = 22, UE = 32, XPERM = 4;
   static constexpr int RUN = 32;        // x run length (elements) of a unit
-  static constexpr bool kStaged = true;   // rows live in one blob (LDS-staged GEMV)
 
   __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
     const uint8_t* blk = a.w + n * a.rb + (int64_t)(k0 >> 5) * BB;
@@ -568,7 +563,6 @@ struct FQ50 {
 struct FQ50S {
   static constexpr int QK = 32, BB = 16, UE = 32, XPERM = 8;
   static constexpr int RUN = 32;        // x run length (elements) of a unit
-  static constexpr bool kStaged = false;   // rows live in one blob (LDS-staged GEMV)
 
   __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
     const int64_t off = n * a.rb + (k0 >> 1);
@@ -616,7 +610,6 @@ struct FQ50S {
 struct FMLX {
   static constexpr int QK = 32, BB = 16, UE = 32, XPERM = 8;
   static constexpr int RUN = 32;        // x run length (elements) of a unit
-  static constexpr bool kStaged = false;   // rows live in one blob (LDS-staged GEMV)
 
   __device__ static void dec32(const QArgs& a, int64_t n, int k0, float (&w)[32]) {
     const u32x4 q = ld16(a.w + n * a.rb + (k0 >> 1));

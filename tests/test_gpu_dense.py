@@ -98,10 +98,9 @@ def test_gemv_dot2_m1(dev, fmt, N, K):
     y = wt.qmm(xt, path="gemv", out_dtype=torch.float32).cpu().numpy()
     check(y, x, wt.W, f"{fmt} gemv N={N} K={K}")
     # every lanes-per-row choice and every kernel variant (1 = register ring with an
-    # LDS row combine, 2 = LDS-staged tiles (formats without staging fall back to
-    # the ring), 3 = wave rows with buffer loads (16/32/64 lanes; shapes needing
+    # LDS row combine, 3 = wave rows with buffer loads (16/32/64 lanes; shapes needing
     # more than 4 units per lane fall back to the ring))
-    for variant in (1, 2, 3):
+    for variant in (1, 3):
         for L in ((0, 16, 32, 64) if variant == 3 else (0, 16, 32, 48, 64, 128, 256)):
             yl = wt.qmm(xt, path="gemv", out_dtype=torch.float32, opts=L | (variant << 36)).cpu().numpy()
             check(yl, x, wt.W, f"{fmt} gemv L={L} variant={variant}")
