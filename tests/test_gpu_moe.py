@@ -81,6 +81,20 @@ def test_moe_routed_small_t(dev, E, k, T, x_scale):
     run_case(dev, T, E=E, k=k, H=512, I=256, gs=64, seed=E + T, x_scale=x_scale)
 
 
+@pytest.mark.parametrize("E,k,T,x_scale", [(4, 2, 16, 1.0), (8, 2, 12, 1.0), (16, 4, 8, 1.0), (16, 2, 12, 1e-3),
+                                             (128, 8, 16, 30.0)])
+def test_moe_many_routes_per_expert(dev, E, k, T, x_scale):
+    # 8 <= T <= 16 on the per-route path: four experts at top-2 over 16 tokens put
+    # about 8 routes on each expert (one expert read by many workgroups at once);
+    # tiny and large activations exercise the per-route scaling of silu(g)*u
+    run_case(dev, T, E=E, k=k, H=512, I=256, gs=64, seed=3 * E + T, x_scale=x_scale)
+
+
+@pytest.mark.parametrize("T", [8, 12])
+def test_moe_config5_mid_t(dev, T):
+    run_case(dev, T, E=128, k=8, H=2048, I=768, gs=64, seed=300 + T)
+
+
 @pytest.mark.parametrize("gs", [32, 64, 128, 256])
 def test_moe_group_sizes(dev, gs):
     # K of gate/up 512 and of down 256: the x-stationary expert kernels with 2 and 1
@@ -159,7 +173,13 @@ def test_gguf_moe_small(dev, T):
     run_gguf_case(dev, T, E=8, k=2, H=512, I=256, seed=50 + T)
 
 
-@pytest.mark.parametrize("T", [1, 16, 256])
+@pytest.mark.parametrize("E,k,T", [(4, 2, 16), (16, 4, 8), (8, 2, 11)])
+def test_gguf_moe_many_routes_per_expert(dev, E, k, T):
+    # per-route few-token path (Q4_K gate/up, Q6_K down) with many routes per expert
+    run_gguf_case(dev, T, E=E, k=k, H=512, I=256, seed=70 + E + T)
+
+
+@pytest.mark.parametrize("T", [1, 8, 16, 256])
 def test_gguf_moe_qwen3_shape(dev, T):
     # Qwen3-MoE-like: 128 experts, top-8, H = 2048, I = 768; at T = 256 every 4th token
     # (64 tokens) checked
