@@ -170,7 +170,7 @@ __global__ __launch_bounds__(256) void k_gemv_dot2(QArgs a, const XT* x, void* y
 // reduce across its L lanes with DPP (quad_perm, row mirrors, row_bcast 15/31) —
 // no LDS, no barrier — and the row's last lane stores it.
 template <class F, int UPT, int D, typename XT, typename YT, int NB>
-__global__ __launch_bounds__(256) void k_gemv_w(WaveBatchT<NB> bt, uint32_t sb, const XT* x, int lshift) {
+__device__ __forceinline__ void gemv_w_body(const WaveBatchT<NB>& bt, uint32_t sb, const XT* x, int lshift) {
   // this workgroup's matrix: the batch entry whose block range holds blockIdx.x
   // (uniform; single-matrix launches are batches of one, NB = 1)
   int mi = 0;
@@ -273,6 +273,29 @@ __global__ __launch_bounds__(256) void k_gemv_w(WaveBatchT<NB> bt, uint32_t sb, 
     rw += D * dw;
     rs += D * ds;
   }
+}
+
+template <class F, int UPT, int D, typename XT, typename YT, int NB>
+__global__ __launch_bounds__(256) void k_gemv_w(WaveBatchT<NB> bt, uint32_t sb, const XT* x, int lshift) {
+  gemv_w_body<F, UPT, D, XT, YT, NB>(bt, sb, x, lshift);
+}
+
+// One matrix with its arguments as scalars, which the dispatch can preload into
+// SGPRs (a structure argument is always read from memory first, a round trip on the
+// critical path of a short launch); the most used first.
+template <class F, int UPT, int D, typename XT, typename YT>
+__global__ __launch_bounds__(256) void k_gemv_w1(const uint8_t* w, int64_t rb, int K, const XT* x, void* y, int N,
+                                                 int lshift, uint32_t sb, int64_t ldy, const uint16_t* sc,
+                                                 const uint16_t* bi, const uint8_t* aux, int gs) {
+  WaveBatchT<1> bt;
+  bt.n = 1;
+  bt.b0[0] = 0;
+  bt.b0[1] = (int)gridDim.x;
+  bt.a[0] = QArgs{w, aux, sc, bi, rb, gs, K};
+  bt.y[0] = y;
+  bt.ldy[0] = ldy;
+  bt.N[0] = N;
+  gemv_w_body<F, UPT, D, XT, YT, 1>(bt, sb, x, lshift);
 }
 
 // ------------------------------------------------------------------ M<=16 GEMV on MFMA
@@ -652,8 +675,14 @@ struct GemvWaveRun {
       acc += (int)g;
     }
     bt.b0[b.n] = acc;
-    hipLaunchKernelGGL((k_gemv_w<F, UPT, D, f16, YT, NB>), dim3((unsigned)acc, (unsigned)M), dim3(256), 0, st,
-                       bt, sb, (const f16*)x, lshift);
+    if constexpr (NB == 1) {
+      const QArgs& a = bt.a[0];
+      hipLaunchKernelGGL((k_gemv_w1<F, UPT, D, f16, YT>), dim3((unsigned)acc, (unsigned)M), dim3(256), 0, st, a.w,
+                         a.rb, a.K, (const f16*)x, bt.y[0], bt.N[0], lshift, sb, bt.ldy[0], a.s, a.b, a.aux, a.gs);
+    } else {
+      hipLaunchKernelGGL((k_gemv_w<F, UPT, D, f16, YT, NB>), dim3((unsigned)acc, (unsigned)M), dim3(256), 0, st,
+                         bt, sb, (const f16*)x, lshift);
+    }
     return hipGetLastError();
   }
   template <int UPT, typename YT>
