@@ -35,9 +35,12 @@ constexpr int rec_words() {     // packed x record of one unit, in dwords (16-by
 
 }  // namespace
 
+// (the arguments are scalars, which the dispatch preloads into SGPRs)
 template <class F, typename YT>
-__global__ __launch_bounds__(256) void k_gemv_t(QArgs a, const f16* x, int M, YT* y, int N, int cpl, int ntiles) {
+__global__ __launch_bounds__(256) void k_gemv_t(const uint8_t* w, int64_t rbytes, int Kx, const f16* x, int M, YT* y,
+                                                int N, int cpl, int ntiles) {
   extern __shared__ __attribute__((aligned(16))) uint8_t sm[];
+  const QArgs a{w, nullptr, nullptr, nullptr, rbytes, 0, Kx};
   constexpr int RW = rec_words<F>();
   const int t = threadIdx.x, wv = t >> 6, lane = t & 63;
   const int K = a.K, U = K / F::UE;
@@ -145,10 +148,10 @@ hipError_t run_tile(const QArgs& a, const void* x, void* y, bool y_f32, int64_t 
   if (o.grid_cap > 0 && o.grid_cap < grid) grid = o.grid_cap;
   if (grid > ntiles) grid = ntiles;
   if (y_f32)
-    hipLaunchKernelGGL((k_gemv_t<F, float>), dim3((unsigned)grid), dim3(256), lds, st, a, (const f16*)x, (int)M,
+    hipLaunchKernelGGL((k_gemv_t<F, float>), dim3((unsigned)grid), dim3(256), lds, st, a.w, a.rb, a.K, (const f16*)x, (int)M,
                        (float*)y, N, cpl, ntiles);
   else
-    hipLaunchKernelGGL((k_gemv_t<F, f16>), dim3((unsigned)grid), dim3(256), lds, st, a, (const f16*)x, (int)M,
+    hipLaunchKernelGGL((k_gemv_t<F, f16>), dim3((unsigned)grid), dim3(256), lds, st, a.w, a.rb, a.K, (const f16*)x, (int)M,
                        (f16*)y, N, cpl, ntiles);
   return hipGetLastError();
 }
