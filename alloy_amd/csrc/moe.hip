@@ -584,9 +584,14 @@ static hipError_t combine(const MoeArgs& m, const MoeLayout& L, hipStream_t st) 
 constexpr int kRoutedTokens = 16;
 
 template <class F, int UPT, int MODE, int VPL>
-__global__ __launch_bounds__(256) void k_gemv_routed(QArgs a, uint32_t sb, int32_t* idx, float* wts,
-                                                     const float* logits, int E, int top_k, const void* xsrc, int N,
-                                                     float* ys, int gx, int lshift) {
+// (arguments as scalars, the first dependent loads' inputs first: the dispatch preloads
+// the leading ones into SGPRs)
+__global__ __launch_bounds__(256) void k_gemv_routed(const float* logits, int gx, int E, int top_k, int lshift,
+                                                     const uint8_t* aw, const uint16_t* as, const uint16_t* ab,
+                                                     int64_t arb, int aK, int N, uint32_t sb, const void* xsrc,
+                                                     float* ys, int32_t* idx, float* wts, const uint8_t* aaux,
+                                                     int ags) {
+  QArgs a{aw, aaux, as, ab, arb, ags, aK};
   const int r = (int)blockIdx.x / gx, bx = (int)blockIdx.x - r * gx;
   int e;
   if constexpr (VPL > 0) {
@@ -740,8 +745,8 @@ static hipError_t launch_routed(const QArgs& a, uint32_t sb, int32_t* idx, float
   if (vpl < 0) return hipErrorNotSupported;
   auto go = [&](auto u, auto v) {
     constexpr int UP = decltype(u)::value, VP = decltype(v)::value;
-    hipLaunchKernelGGL((k_gemv_routed<F, UP, MODE, VP>), grid, block, 0, st, a, sb, idx, wts, logits, E, top_k, xsrc, N,
-                       ys, (int)gx, lshift);
+    hipLaunchKernelGGL((k_gemv_routed<F, UP, MODE, VP>), grid, block, 0, st, logits, (int)gx, E, top_k, lshift, a.w, a.s,
+                       a.b, a.rb, a.K, N, sb, xsrc, ys, idx, wts, a.aux, a.gs);
     return hipGetLastError();
   };
   using I1 = std::integral_constant<int, 1>;
