@@ -183,7 +183,7 @@ def roofline(mats, xs, ys, qmm, dev, total_bytes, step_s):
               for (K, N), v in per.items()}
     return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
-            "kernel": "k_gemv_w<FQ4K> (Q4_K M=1 wave-row GEMV)",
+            "kernel": "k_gemv_w1<FQ4K> (Q4_K M=1 wave-row GEMV, single-matrix entry)",
             "bytes_per_launch": round(total_bytes / launches),
             "avg_launch_us": round(step_s / launches * 1e6, 3), "per_shape": shapes,
             "per_shape_frac": round(total_bytes / tot_t / 1e9 / HBM_PEAK_GBS, 4),
