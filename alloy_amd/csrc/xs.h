@@ -654,7 +654,7 @@ __device__ __forceinline__ float xs_act(int act, float v) {
 // stored.  Dynamic LDS: Xs[W][NS/8][NCH][16] + red[W][RT][64][4 NM] (+ tmx[W][16]
 // + tsc[16] for MODE 2) floats.
 template <class P, int MODE, int NS, int TT, int RT, bool PIPE, class YT, bool MP = false>
-__global__ __launch_bounds__(MP ? 64 * XsMPW<P>::value : 1024) void k_gemv_xs(XsJob j) {
+__device__ __forceinline__ void xs_body(const XsJob& j) {
   static_assert(!MP || (MODE == 0 && RT == 1 && !PIPE && XsIsDQ<P>::value), "multi-pass: dense, one tile, dequantising");
   constexpr int NM = (MODE == 1 || MODE == 3) ? 2 : 1;   // weight matrices per output
   constexpr int UPW = NS / 8;                    // units per wave
@@ -979,6 +979,33 @@ __global__ __launch_bounds__(MP ? 64 * XsMPW<P>::value : 1024) void k_gemv_xs(Xs
   run(std::integral_constant<int, TT>());
 }
 
+template <class P, int MODE, int NS, int TT, int RT, bool PIPE, class YT, bool MP = false>
+__global__ __launch_bounds__(MP ? 64 * XsMPW<P>::value : 1024) void k_gemv_xs(XsJob j) {
+  xs_body<P, MODE, NS, TT, RT, PIPE, YT, MP>(j);
+}
+
+// MODE 0 with the job's fields as scalar arguments, those the first loads need first:
+// the dispatch preloads the leading ones into SGPRs, where a structure argument is
+// read from memory before any load can be addressed.
+template <class P, int NS, int TT, int RT, bool PIPE, class YT, bool MP = false>
+__global__ __launch_bounds__(MP ? 64 * XsMPW<P>::value : 1024) void k_gemv_xs0(
+    const uint8_t* w, int64_t rb, int K, const void* x, int W, int N, int M, int kp, int ku_split, uint32_t xbytes,
+    int xld, void* y, const uint16_t* s, const uint16_t* b, uint32_t sb, int gs, const uint8_t* aux) {
+  XsJob j{};
+  j.a = QArgs{w, aux, s, b, rb, gs, K};
+  j.x = x;
+  j.xbytes = xbytes;
+  j.xld = xld;
+  j.M = M;
+  j.N = N;
+  j.y = y;
+  j.sb = sb;
+  j.W = W;
+  j.kp = kp;
+  j.ku_split = ku_split;
+  xs_body<P, 0, NS, TT, RT, PIPE, YT, MP>(j);
+}
+
 // Host launcher.  hipErrorNotSupported when the shape does not fit the kernel
 // (K not a multiple of 256, over 8192 except for the multi-pass dense kernel of the
 // dequantising providers, offsets of 2 GiB or more): the caller then
@@ -1038,7 +1065,11 @@ hipError_t launch_xs(const XsJob& j, int64_t tiles_y, int64_t cap, int rt, hipSt
     jw.W = W;
     jw.kp = kp;
     jw.ku_split = ksplit;
-    hipLaunchKernelGGL(kern, grid, block, lds, st, jw);
+    if constexpr (MODE == 0)
+      hipLaunchKernelGGL(kern, grid, block, lds, st, jw.a.w, jw.a.rb, jw.a.K, jw.x, jw.W, jw.N, jw.M, jw.kp,
+                         jw.ku_split, jw.xbytes, jw.xld, jw.y, jw.a.s, jw.a.b, jw.sb, jw.a.gs, jw.a.aux);
+    else
+      hipLaunchKernelGGL(kern, grid, block, lds, st, jw);
     return hipGetLastError();
   };
   // whether the tiles outnumber the resident workgroups of the one-pass kernel
@@ -1054,14 +1085,14 @@ hipError_t launch_xs(const XsJob& j, int64_t tiles_y, int64_t cap, int rt, hipSt
       constexpr int TT = decltype(ttc)::value;
       using YT = decltype(yt);
       if constexpr (XsIsDQ<P>::value && !P::WIDE) {
-        if (kp > 1) return go(k_gemv_xs<P, 0, 8, TT, 1, false, YT, true>, false);
+        if (kp > 1) return go(k_gemv_xs0<P, 8, TT, 1, false, YT, true>, false);
       }
       if constexpr (P::WIDE) {
-        if (ns == 16) return go(k_gemv_xs<P, 0, 16, TT, 1, false, YT>, false);
-        if (rt == 2) return go(k_gemv_xs<P, 0, 8, TT, 2, true, YT>, true);
+        if (ns == 16) return go(k_gemv_xs0<P, 16, TT, 1, false, YT>, false);
+        if (rt == 2) return go(k_gemv_xs0<P, 8, TT, 2, true, YT>, true);
       }
-      if (many(k_gemv_xs<P, 0, 8, TT, 1, false, YT>)) return go(k_gemv_xs<P, 0, 8, TT, 1, true, YT>, true);
-      return go(k_gemv_xs<P, 0, 8, TT, 1, false, YT>, false);
+      if (many(k_gemv_xs0<P, 8, TT, 1, false, YT>)) return go(k_gemv_xs0<P, 8, TT, 1, true, YT>, true);
+      return go(k_gemv_xs0<P, 8, TT, 1, false, YT>, false);
     };
     if (j.y_f32) return tt == 1 ? pick(I1(), 0.f) : tt == 2 ? pick(I2(), 0.f) : pick(I4(), 0.f);
     return tt == 1 ? pick(I1(), (f16)0) : tt == 2 ? pick(I2(), (f16)0) : pick(I4(), (f16)0);
