@@ -100,6 +100,16 @@ def torch_blocks(fmt: str, N: int, K: int, seed: int, device) -> torch.Tensor:
     return blk.view(N, nb * bb)
 
 
+def torch_q8_0_split(N: int, K: int, seed: int, device):
+    """Q8_0 in the reference operator's split layout (int8 quants [N, K], fp16 scales
+    [N, K/32]) with the wire blocks' distribution: quants uniform in [-127, 127], scales
+    |N(0,1)| * 0.01 — the same 34 bytes per 32 weights."""
+    g = _gen(seed, device)
+    qweight = torch.randint(-127, 128, (N, K), generator=g, device=device, dtype=torch.int8)
+    scales = _abs_normal_f16((N, K // 32), D_SCALE["q8_0"], g, device)
+    return qweight, scales
+
+
 def torch_mlx(N: int, K: int, group_size: int, seed: int, device):
     g = _gen(seed, device)
     qweight = torch.randint(0, 256, (N, K // 2), generator=g, device=device, dtype=torch.uint8)

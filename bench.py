@@ -399,6 +399,17 @@ def other_configs(dev, qmm, eager=False):
                 "frac_hbm_peak": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
 
     out["config1_q8_0_4096x4096_M1"] = gemv_case("q8_0", 4096, 4096, 1, 300)
+    # the same weights in the layout the reference's gguf_q8_0_mm takes (int8 quants and
+    # fp16 scales in separate arrays, same bytes): its drop-in call
+    nbytes = formats.row_bytes("q8_0", 4096) * 4096
+    ws = [synth.torch_q8_0_split(4096, 4096, 310 + i, dev) for i in range(max(2, -(-MIN_ROTATE_BYTES // nbytes)))]
+    x1 = synth.torch_x(1, 4096, 300, dev)
+    y1 = torch.empty((1, 4096), dtype=torch.float32, device=dev)
+    t = _rotating_time(dev, lambda w: qmm("q8_0_split", x1, w[0], scales=w[1], N=4096, out=y1), ws, eager=eager)
+    del ws
+    out["config1_q8_0_split_4096x4096_M1"] = {"us": round(t * 1e6, 2), "GBps": round(nbytes / t / 1e9, 1),
+                                              "frac_hbm_peak": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4),
+                                              "layout": "split (the reference op's qweight + scales)"}
     for M in (4, 16):
         out[f"config2_q4_k_M{M}"] = {f"{K}x{N}": gemv_case("q4_k", K, N, M, 350 + K + N)
                                      for _, K, N in LLAMA32_3B[:2] + LLAMA32_3B[4:5] + LLAMA32_3B[6:] + [LM_HEAD]}

@@ -364,6 +364,21 @@ def test_q8_0_config1(dev):
     _sampled("q8_0", 4096, 4096, 1, dev, seed=0)
 
 
+def test_q8_0_split_config1(dev):
+    """Config 1 through the reference operator's layout (gguf_q8_0_mm: int8 qweight and
+    fp16 scales), as bench.py times it: the same blocks split by the oracle, full shape,
+    sampled rows against the oracle's decode of the wire blocks."""
+    N = K = 4096
+    rng = np.random.default_rng(1)
+    blob = synth.numpy_blocks("q8_0", N, K, rng)
+    qw, sc = oq.split_q8_0(blob, K)
+    x = synth.numpy_x(1, K, rng)
+    y = torch.ops.alloy.gguf_q8_0_mm(torch.from_numpy(x).to(dev), torch.from_numpy(qw).to(dev),
+                                     torch.from_numpy(sc).to(dev)).float().cpu().numpy()
+    rows = np.unique(np.concatenate([rng.integers(0, N, 48), [0, N - 1]]))
+    check(y[:, rows], x, oq.dequant("q8_0", blob[rows], K), f"q8_0 split config 1 {N}x{K}")
+
+
 @pytest.mark.parametrize("M", [512, 2048, 4096])
 @pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 14336), (14336, 4096)])
 def test_q4_k_prefill_shapes(dev, M, K, N):
