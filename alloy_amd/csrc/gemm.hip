@@ -151,11 +151,22 @@ __device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t r, uint8_t* ld
 }
 // s_waitcnt immediate: vmcnt(n) (n < 64), no wait on the export counter, lgkmcnt(l)
 constexpr int waitcnt_enc(int n, int l) { return 0x0070 | (l << 8) | (n & 15) | ((n >> 4) << 14); }
-// workgroup barrier of the swizzled GEMM: this wave's loads but the last n and all
-// its LDS accesses complete, then s_barrier, with no instruction moved across
+// Workgroup barrier of the swizzled GEMMs: this wave's loads but the last n and all
+// its LDS accesses complete, then s_barrier, with no instruction moved across.  The
+// GEMMs use n = 0.  A partial count (only the loads issued after a stage's
+// buffer-to-LDS copy outstanding) assumes that the copies and the plain loads retire
+// in issue order; with it the 4096 x 14336 x 4096 Q4_K product differed between
+// repeated runs (60 of 400), with the full wait in none of 400.
 template <int N>
 __device__ __forceinline__ void step_barrier() {
   __builtin_amdgcn_s_waitcnt(waitcnt_enc(N, 0));
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+// the same with LDS accesses only (loads stay in flight)
+__device__ __forceinline__ void step_barrier_lds() {
+  __builtin_amdgcn_s_waitcnt(waitcnt_enc(63, 0));
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
@@ -215,7 +226,7 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, 
   const float smul = h ? 1048576.f : 16777216.f;      // 2^20 (high nibbles hold 16q) or 2^24
   const int swb = lds_swz(br);
   const int c0 = 4 * h + (BPT / 8) * part;            // first logical chunk this thread writes
-  u32x4 raw[3][LPT];                                  // pair slots (pair index mod 3)
+  u32x4 raw[4][LPT];                                  // pair slots (pair index mod 4)
   u32x4 hdr[3];                                       // super-block headers (index mod 3)
   auto rload = [&](int pair, u32x4 (&slot)[LPT]) {    // LPT loads
     const int sbi = pair >> 2;
@@ -273,18 +284,21 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, 
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   // step kt (J = kt % 12, a compile-time constant): MFMAs on x stage kt%3 and weight
-  // stage kt%2; x(kt+2) copied into stage (kt+2)%3 first; pair kt+1 (slot (kt+1)%3,
-  // header of super-block (kt+1)/4 in the slot of its parity) dequantised into weight
-  // stage (kt+1)%2; pair kt+4 loaded into the freed slot last (and, when it starts a
-  // super-block, that super-block's header).
+  // stage kt%2; first x(kt+2) copied into stage (kt+2)%3 and pair kt+4 loaded into
+  // ring slot kt%4 (its pair kt was consumed by the previous step; and, when it
+  // starts a super-block, that super-block's header), so they have the whole step to
+  // land before the closing full wait; pair kt+1 (slot (kt+1)%4, header of
+  // super-block (kt+1)/4) dequantised into weight stage (kt+1)%2.
   auto step = [&](auto Jc, int kt) {
     constexpr int J = decltype(Jc)::value;
-    constexpr int P1 = (J + 1) & 3, R1 = (J + 1) % 3;            // pair within its super-block, ring slot
+    constexpr int P1 = (J + 1) & 3, R1 = (J + 1) & 3, RN = J & 3;   // pair within its super-block, ring slots
     constexpr int H1 = ((J + 1) >> 2) % 3, HN = ((J >> 2) + 1) % 3;  // header of pair kt+1 / loaded now
-    constexpr bool hnow = (J & 3) == 0, hprev = (J & 3) == 1;  // header loads at this / the previous step
+    constexpr bool hnow = (J & 3) == 0;                        // a header load at this step
     const uint8_t* xc = XS[J % 3];
     const uint8_t* wc = WS[J & 1];
     xcopy(kt + 2, XS[(J + 2) % 3]);
+    rload(kt + 4, raw[RN]);
+    if constexpr (hnow) hload((kt >> 2) + 1, hdr[HN]);   // its slot's last use: super-block kt/4 - 2
     float s, c;
     scale(hdr[H1], P1, s, c);
     frag(xc, wc, 0, 0);
@@ -299,20 +313,20 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, 
           acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cs][i], bf[cs][jn], acc[i][jn], 0, 0, 0);
       if (CPT == 4 || (ks & 1) == 0) deq(raw[R1], CPT == 4 ? ks : ks >> 1, s, c, WS[(J + 1) & 1]);
     }
-    // the prefetch loads stay behind this step's x copy (the wait below counts on it)
     __builtin_amdgcn_sched_barrier(0);
-    rload(kt + 4, raw[R1]);
-    if constexpr (hnow) hload((kt >> 2) + 1, hdr[HN]);   // its slot's last use: super-block kt/4 - 2
-    // x(kt+1), copied at the top of step kt-1, is done once at most the loads issued
-    // after it are outstanding: the prefetch of step kt-1, x(kt+2) and this prefetch
-    step_barrier<2 * LPT + MI + (hnow ? 1 : 0) + (hprev ? 1 : 0)>();
+    // every load lands before a full wait at the end of every even step, so each has
+    // one or two steps: x(k) (issued at step k-2) is needed at step k, pair p (step
+    // p-4) at step p-1, a header (step 4s-4) at step 4s-1; odd steps order the LDS
+    // stages only
+    if constexpr ((J & 1) == 0) step_barrier<0>();
+    else step_barrier_lds();
   };
 
-  // prologue: header 0; pairs 0..2 (slots 0..2); x of steps 0 and 1; pair 0
-  // dequantised into weight stage 0; pair 3 into slot 0 (the loop's step-(-1) prefetch)
+  // prologue: header 0; pairs 0..3 (slots 0..3); x of steps 0 and 1; pair 0
+  // dequantised into weight stage 0
   hload(0, hdr[0]);
 #pragma unroll
-  for (int p = 0; p < 3; ++p) rload(p, raw[p]);
+  for (int p = 0; p < 4; ++p) rload(p, raw[p]);
   xcopy(0, xs0);
   xcopy(1, xs1);
   {
@@ -322,8 +336,7 @@ __global__ __launch_bounds__(512) void k_gemm_q4k(QArgs a, const f16* x, int M, 
     for (int j = 0; j < CPT; ++j) deq(raw[0], j, s, c, ws0);
   }
   __builtin_amdgcn_sched_barrier(0);
-  rload(3, raw[0]);
-  step_barrier<MI + LPT>();                          // x(0) done: x(1) and pair 3 may be in flight
+  step_barrier<0>();
   // twelve steps (three super-blocks) per iteration, then 0, 4 or 8 more
   int kt = 0;
   for (; kt + 12 <= KT; kt += 12) {
@@ -700,9 +713,12 @@ __global__ __launch_bounds__(512) void k_gemm_w(GemmArgs ga, const f16* x, int M
     });
     __builtin_amdgcn_sched_barrier(0);
     rload(kt + 4, raw[R1]);
-    // x(kt+1) is done once at most the loads issued after it are outstanding: the
-    // prefetch of step kt-1, x(kt+2) and this prefetch
-    step_barrier<2 * W::NL + MI>();
+    // a full wait at the end of every even step: x(k) (issued at step k-2) is needed at
+    // step k, the weights of step p (issued at the end of step p-4) at step p-1, so a
+    // full wait lies between every load and its first use; odd steps order the LDS
+    // stages only
+    if constexpr ((J & 1) == 0) step_barrier<0>();
+    else step_barrier_lds();
   };
 
   // prologue: steps 0..2 loaded (slots 0..2), x of steps 0 and 1, step 0 decoded into
@@ -714,7 +730,7 @@ __global__ __launch_bounds__(512) void k_gemm_w(GemmArgs ga, const f16* x, int M
   xs_static_for<0, 4>([&](auto chc) { deq(raw[0], chc, 0, ws0); });
   __builtin_amdgcn_sched_barrier(0);
   rload(3, raw[0]);
-  step_barrier<MI + W::NL>();
+  step_barrier<0>();                                     // x(0) and x(1) landed
   int kt = 0;
   for (; kt + 6 <= KT; kt += 6) {
     step(std::integral_constant<int, 0>(), kt + 0);
