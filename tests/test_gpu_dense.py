@@ -151,17 +151,17 @@ def test_gemv_mfma(dev, fmt, M):
     for rg in (1, 2):
         y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=rg << 28).cpu().numpy()
         check(y, x, wt.W, f"{fmt} gemv_mfma M={M} rg={rg}")
-    if fmt in ("q4_k", "q6_k", "mlx_q4", "q8_0", "q5_0") and M <= 16:
+    if fmt in ("q4_k", "q6_k", "mlx_q4", "q8_0", "q5_0", "q8_0_split") and M <= 16:
         # every kernel explicitly: 1 = 16x16x32 tiles, 5 = 4x4x4 broadcast (Q4_K),
         # 6 = x-stationary 16x16x32 (Q4_K), 7 = generic x-stationary (Q4_K, Q6_K, MLX),
         # 8 = x-stationary with fp16-dequantised weights (Q4_K, Q6_K, MLX, Q8_0, Q5_0)
-        variants = {"q4_k": (1, 5, 6, 7, 8), "q8_0": (1, 8), "q5_0": (1, 8)}.get(fmt, (1, 7, 8))
+        variants = {"q4_k": (1, 5, 6, 7, 8), "q8_0": (1, 8), "q5_0": (1, 8), "q8_0_split": (1, 8)}.get(fmt, (1, 7, 8))
         for variant in variants:
             y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=variant << 36).cpu().numpy()
             check(y, x, wt.W, f"{fmt} gemv_mfma M={M} variant={variant}")
 
 
-@pytest.mark.parametrize("fmt", ["q6_k", "q5_0", "q8_0"])
+@pytest.mark.parametrize("fmt", ["q6_k", "q5_0", "q8_0", "q8_0_split"])
 @pytest.mark.parametrize("M", [3, 8, 16])
 @pytest.mark.parametrize("K,N", [(8192, 72), (11008, 33), (14336, 40)])
 def test_gemv_xs_multipass(dev, fmt, M, K, N):
@@ -179,7 +179,7 @@ def test_gemv_xs_multipass(dev, fmt, M, K, N):
     check(y16, x, wt.W, f"{fmt} xs multi-pass fp16 out M={M} K={K} N={N}")
 
 
-@pytest.mark.parametrize("fmt", ["q4_k", "q6_k", "q5_0", "q8_0", "mlx_q4"])
+@pytest.mark.parametrize("fmt", ["q4_k", "q6_k", "q5_0", "q8_0", "q8_0_split", "mlx_q4"])
 @pytest.mark.parametrize("M", [3, 8, 16])
 @pytest.mark.parametrize("K,N,splits", [(2048, 132, 3), (8192, 72, 2), (8192, 72, 5), (11008, 40, 4),
                                         (1024, 40, 7), (2048, 130, 2)])
@@ -358,6 +358,22 @@ def test_q4_k_decode_shapes(dev, K, N, M):
 @pytest.mark.parametrize("M", [1, 8])
 def test_q6_k_q5_0_decode_shapes(dev, fmt, K, N, M):
     _sampled(fmt, N, K, M, dev, seed=K + 3 * N + M)
+
+
+@pytest.mark.parametrize("fmt,M,K,N,runs", [("q4_k", 4096, 14336, 4096, 40), ("q8_0", 2048, 14336, 4096, 20)])
+def test_gemm_repeatable(dev, fmt, M, K, N, runs):
+    """Repeated prefill GEMMs on the same inputs give bit-identical outputs: a stage
+    barrier that let a wave read an LDS stage before its buffer-to-LDS copy landed
+    made 4096 x 14336 x 4096 differ in 15 % of runs."""
+    w = synth.torch_blocks(fmt, N, K, 17, dev)
+    x = synth.torch_x(M, K, 18, dev)
+    ref = alloy_amd.qmm(fmt, x, w, out_dtype=torch.float32, path="gemm")
+    y = torch.empty_like(ref)
+    diff = 0
+    for _ in range(runs):
+        alloy_amd.qmm(fmt, x, w, out=y, path="gemm")
+        diff += 0 if torch.equal(y, ref) else 1
+    assert diff == 0, f"{fmt} {M}x{K}x{N}: {diff} of {runs} repeated GEMMs differ from the first"
 
 
 def test_q8_0_config1(dev):
