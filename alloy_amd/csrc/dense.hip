@@ -1075,6 +1075,10 @@ static hipError_t launch_xs_job(int fmt, XsJob j, const Opts& o, hipStream_t st,
     if (fmt == F_Q6_K) return launch_xs<XsDQ<XsQ6KW>, 0>(j, 0, dcap, rt, st);
     if (fmt == F_Q5_0) return launch_xs<XsDQ<XsQ50>, 0>(j, 0, dcap, rt, st);
     if (fmt == F_Q8_0) return launch_xs<XsDQ<XsQ80>, 0>(j, 0, dcap, rt, st);
+    if (fmt == F_Q8_0S) {
+      j.sb = (uint32_t)(a.K / 16);               // fp16 scales per row
+      return launch_xs<XsDQ<XsQ80S>, 0>(j, 0, dcap, rt, st);
+    }
   } else {
     if (fmt == F_Q4_K) return launch_xs<XsQ4K, 0>(j, 0, cap, o.row_groups, st);
     if (fmt == F_Q6_K) return launch_xs<XsQ6K, 0>(j, 0, cap, o.row_groups, st);
@@ -1148,8 +1152,8 @@ hipError_t launch_glu_combine(int act, const float* g, const float* u, void* y, 
 //   Q4_K  tall (N >= 32768) and 3 <= M <= 6: 4x4x4 broadcast kernel; K <= 8192: the
 //         x-stationary kernel with fp16-dequantised weights (8); else the Q4_K
 //         x-stationary kernel
-//   Q6_K, Q5_0, Q8_0 (wire blocks)  x-stationary with fp16-dequantised weights (K over
-//         4096: in passes over K)
+//   Q6_K, Q5_0, Q8_0 (wire blocks) and split Q8_0  x-stationary with fp16-dequantised
+//         weights (K over 4096: in passes over K)
 //   MLX   generic x-stationary (exact products); N >= 12288: the dequantising
 //         provider with 16-byte loads, one workgroup per CU looping over the tiles
 //   other formats (and shapes the above do not take): 16x16x32 kernel
@@ -1158,7 +1162,7 @@ static int mfma_variant(int fmt, int64_t M, int64_t N, int64_t K) {
     if (N >= 32768 && M >= 3 && M <= 6) return 5;
     return K <= 8192 ? 8 : 6;
   }
-  if (fmt == F_Q6_K || fmt == F_Q5_0 || fmt == F_Q8_0) return 8;
+  if (fmt == F_Q6_K || fmt == F_Q5_0 || fmt == F_Q8_0 || fmt == F_Q8_0S) return 8;
   if (fmt == F_MLX) return N >= 12288 ? 8 : 7;
   return 1;
 }
@@ -1172,7 +1176,7 @@ static int mfma_variant(int fmt, int64_t M, int64_t N, int64_t K) {
 // K = 8192 takes the Q4_K x-stationary kernel, which does not split.
 static int gemv_splits(int fmt, int64_t M, int64_t N, int64_t K) {
   if (M < 8 || M > 16 || K < 4096 || K % 256 || (fmt == F_Q4_K && K > 8192)) return 1;
-  if (fmt != F_Q4_K && fmt != F_Q6_K && fmt != F_Q5_0 && fmt != F_Q8_0 && fmt != F_MLX) return 1;
+  if (fmt != F_Q4_K && fmt != F_Q6_K && fmt != F_Q5_0 && fmt != F_Q8_0 && fmt != F_Q8_0S && fmt != F_MLX) return 1;
   const int64_t tiles = (N + 15) / 16;
   return tiles <= 64 ? 4 : tiles <= 128 ? 2 : 1;
 }

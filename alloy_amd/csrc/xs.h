@@ -480,6 +480,40 @@ struct XsQ80 {
   }
 };
 
+// Q8_0 in the split layout (int8 quants [N, K], fp16 scales [N, K/32]): lane kq of a
+// 256-element unit takes its 64 contiguous quants (four aligned 16-byte loads) and its
+// two blocks' scales (one dword); the chains and the dequant are XsQ80's.
+struct XsQ80S {
+  static constexpr int NCH = 8;
+  static constexpr bool WIDE = false;
+  struct Raw { uint32_t w[16]; uint32_t d; };
+  __device__ static void load(const Src& src, uint32_t rw, uint32_t rs, int unit, int kq, Raw& r) {
+    const uint32_t bo = rw + (uint32_t)unit * 256u + 64u * (uint32_t)kq;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 a = bld16(src.w, bo + 16u * i);
+      r.w[4 * i] = a.x; r.w[4 * i + 1] = a.y; r.w[4 * i + 2] = a.z; r.w[4 * i + 3] = a.w;
+    }
+    r.d = bld4(src.s, rs + (uint32_t)unit * 16u + 4u * (uint32_t)kq);
+  }
+  __device__ static f16x8 xload(__amdgpu_buffer_rsrc_t xr, uint32_t off, int S, int kq) {
+    return xs_x8(xr, off + 2u * (uint32_t)(64 * kq + 8 * S));
+  }
+  template <int C>
+  __device__ static void dq(const f16x8* xu, const Raw& r, f32x4& acc) {
+    constexpr int blk = C >> 2, wi = 2 * (C & 3);
+    const float dd = h2f(blk ? r.d >> 16 : r.d), s = dd * 16777216.f, c = -128.f * dd;
+    uint32_t b[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      // int8 q as the byte q + 128 (fp16 denormal (q + 128) 2^-24): elements 2p, 2p + 1
+      const uint32_t v = __builtin_amdgcn_perm(0u, r.w[8 * blk + wi + (p >> 1)], (p & 1) ? 0x0c030c02u : 0x0c010c00u);
+      b[p] = xs_dq2(v ^ 0x00800080u, s, c);
+    }
+    acc = xs_mfma32(xu[C], u32x4{b[0], b[1], b[2], b[3]}, acc);
+  }
+};
+
 // MLX 4-bit affine with the weights dequantised to fp16 (s q + b, rounded once), any
 // group size 32 << GSH: every lane reads two 16-byte runs of four words (words 4 kq
 // .. + 3 and 16 + 4 kq .. + 3 of the unit; MFMA S takes word 16 (S / 4) + 4 kq + S % 4),
