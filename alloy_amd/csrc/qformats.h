@@ -78,7 +78,12 @@ __device__ __forceinline__ void ld_words_a2(const uint8_t* p, uint32_t (&o)[NW])
 #define MAGIC1 0x3C003C00u   // fp16 1.0 in both halves
 
 // Bit-field helpers emitted as single VOP3 instructions (the mask lives in an SGPR,
-// the other operands in VGPRs: one constant-bus read, as gfx9 allows).
+// the other operands in VGPRs: one constant-bus read, as gfx9 allows).  The plain
+// expressions compile to an AND and an OR with a literal per use instead (measured
+// on the streaming GEMVs: 2-10 % more instructions).  Inline asm hides these writes
+// from the hazard recognizer, so they serve only kernels without MFMAs: the decode
+// GEMVs, the tile-staged GEMV and the T = 1 routed GEMV; the MFMA kernels decode
+// through plain expressions.
 __device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {   // (a & mask) | (b & ~mask)
   uint32_t r;
   asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(b));
