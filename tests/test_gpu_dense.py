@@ -127,6 +127,30 @@ def test_gemv_tile_staged(dev, fmt, M, N, K):
     check(y, x, wt.W, f"{fmt} tile via the MFMA-path variant M={M} N={N} K={K}")
 
 
+@pytest.mark.parametrize("fmt", ["q6_k", "q5_0", "q8_0"])
+@pytest.mark.parametrize("N,K", [(1, 4096), (77, 14336), (1001, 4096), (4099, 14336), (3, 8192), (513, 2048)])
+def test_gemv_tile_ring_m1(dev, fmt, N, K):
+    """M = 1 through the tile ring (depth 2 / 4: 1, 2 or 4 rows per tile by the row's
+    unit count, two or four tiles in flight, rows summed across waves), the four-row
+    tile kernel (depth 1) and the automatic choice (depth 0: the ring for Q6_K at
+    K = 14336 and where the four-row tile would pass 48 KiB, Q8_0 at K = 14336),
+    against the oracle; partial last tiles and fewer tiles than workgroups."""
+    rng = np.random.default_rng(N * 3 + K)
+    wt = Weight(fmt, N, K, rng, dev)
+    x = synth.numpy_x(1, K, rng)
+    xt = torch.from_numpy(x).to(dev)
+    ys = {}
+    for depth in (0, 1, 2, 4):
+        for od in (torch.float32, torch.float16):
+            y = wt.qmm(xt, path="gemv", out_dtype=od, opts=(4 << 36) | (depth << 32)).float().cpu().numpy()
+            check(y, x, wt.W, f"{fmt} tile ring M=1 N={N} K={K} depth={depth} {od}")
+            ys[depth, od] = y
+    # four and two tiles in flight: the same arithmetic in the same order
+    assert np.array_equal(ys[4, torch.float32], ys[2, torch.float32]), "ring depth changed the result"
+    y = wt.qmm(xt, out_dtype=torch.float32).cpu().numpy()
+    check(y, x, wt.W, f"{fmt} default route M=1 N={N} K={K}")
+
+
 @pytest.mark.parametrize("fmt", FORMATS)
 def test_gemv_dot2_multi_row_and_f32_x(dev, fmt):
     rng = np.random.default_rng(7)
