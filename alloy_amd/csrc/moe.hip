@@ -449,15 +449,28 @@ __global__ __launch_bounds__(256) void k_down(QArgs dn, const f16* h, const int3
   }
 }
 
+// Slots in groups of 8: the group's weights and partials are all requested before
+// the first is added (a loop that adds each slot as it arrives waits one memory
+// latency per slot), then summed in slot order.
 __global__ __launch_bounds__(256) void k_combine(const float* part, const int32_t* inv,
                                                  const float* wts, float* y, int top_k, int H) {
+  constexpr int G = 8;
   const int64_t t = blockIdx.x;
   const int j = blockIdx.y * 256 + threadIdx.x;
   if (j >= H) return;
   float acc = 0.f;
-  for (int s = 0; s < top_k; ++s) {
-    const int64_t r = t * top_k + s;
-    acc += wts[r] * part[(int64_t)(inv ? inv[r] : r) * H + j];   // no inv: partials in route order
+  for (int s0 = 0; s0 < top_k; s0 += G) {
+    float w[G], p[G];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int64_t r = t * top_k + s0 + i;
+      const bool in = s0 + i < top_k;
+      w[i] = in ? wts[r] : 0.f;
+      p[i] = in ? part[(int64_t)(inv ? inv[r] : r) * H + j] : 0.f;   // no inv: partials in route order
+    }
+#pragma unroll
+    for (int i = 0; i < G; ++i)
+      if (s0 + i < top_k) acc += w[i] * p[i];
   }
   y[t * H + j] = acc;
 }
