@@ -773,8 +773,20 @@ template <typename YT>
 __global__ __launch_bounds__(256) void k_splitk_sum(const float* ws, int S, int64_t mn, YT* y) {
   const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (i >= mn) return;
-  f32x4 acc = *(const f32x4*)(ws + i);
-  for (int z = 1; z < S; ++z) acc += *(const f32x4*)(ws + (int64_t)z * mn + i);
+  // slices in groups of four: the group's loads are all requested before the first
+  // add (one memory latency per group, not per slice); summed in slice order
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int z0 = 0; z0 < S; z0 += 4) {
+    f32x4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {        // past the last slice: the last slice again (unused)
+      const int z = z0 + k < S ? z0 + k : S - 1;
+      v[k] = *(const f32x4*)(ws + (int64_t)z * mn + i);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (z0 + k < S) acc = z0 + k == 0 ? v[k] : acc + v[k];
+  }
   if constexpr (sizeof(YT) == 4) {
     *(f32x4*)((float*)y + i) = acc;
   } else {
