@@ -270,6 +270,10 @@ hipError_t launch_rt(int cpl, const QArgs& a, const void* x, void* y, int N, int
                      hipStream_t st) {
   const void* k = cpl == 1 ? (const void*)k_gemv_rt<F, YT, D, 1> : cpl == 2 ? (const void*)k_gemv_rt<F, YT, D, 2>
                 : cpl == 3 ? (const void*)k_gemv_rt<F, YT, D, 3> : (const void*)k_gemv_rt<F, YT, D, 4>;
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
   int grid = resident_per_cu(k, 256, lds) * cu_count();
   if (cap > 0 && cap < grid) grid = cap;
   if (grid > ntiles) grid = ntiles;

@@ -128,7 +128,8 @@ def test_gemv_tile_staged(dev, fmt, M, N, K):
 
 
 @pytest.mark.parametrize("fmt", ["q6_k", "q5_0", "q8_0"])
-@pytest.mark.parametrize("N,K", [(1, 4096), (77, 14336), (1001, 4096), (4099, 14336), (3, 8192), (513, 2048)])
+@pytest.mark.parametrize("N,K", [(1, 4096), (77, 14336), (1001, 4096), (4099, 14336), (3, 8192), (513, 2048),
+                                 (65, 16384)])
 def test_gemv_tile_ring_m1(dev, fmt, N, K):
     """M = 1 through the tile ring (depth 2 / 4: 1, 2 or 4 rows per tile by the row's
     unit count, two or four tiles in flight, rows summed across waves), the four-row
