@@ -252,8 +252,12 @@ hipError_t run_tile(const QArgs& a, const void* x, void* y, bool y_f32, int64_t 
   if (cpl > kMaxCpl || lds > 160 * 1024) return hipErrorNotSupported;
   const int N = (int)N64;
   const int ntiles = (N + kTileRows - 1) / kTileRows;
-  int grid = resident_per_cu(y_f32 ? (const void*)k_gemv_t<F, float> : (const void*)k_gemv_t<F, f16>, 256, lds) *
-             cu_count();
+  const void* k = y_f32 ? (const void*)k_gemv_t<F, float> : (const void*)k_gemv_t<F, f16>;
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  int grid = resident_per_cu(k, 256, lds) * cu_count();
   if (o.grid_cap > 0 && o.grid_cap < grid) grid = o.grid_cap;
   if (grid > ntiles) grid = ntiles;
   if (y_f32)

@@ -385,20 +385,25 @@ struct FQ6K {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint32_t v = r.ql[i], c = r.qh[i];
-      // 6-bit u in fp16 mantissa bits 4..9 -> value 1 + u/64
-      const uint32_t p0 = bfi(0x03000300u, c << (8 - c0), bfi(0x00F000F0u, v << 4, magic));
-      const uint32_t p1 = bfi(0x03000300u, c >> c0, bfi(0x00F000F0u, v >> 4, magic));
-      const uint32_t p2 = bfi(0x03000300u, c << (4 - c0), and_or(v, 0x00F000F0u, magic));
-      const uint32_t p3 = bfi(0x03000300u, c >> (c0 + 4), bfi(0x00F000F0u, v >> 8, magic));
+      // the nibbles where they lie (bytes 1, 3 moved down by 8), the 2-bit highs moved to
+      // sit above them: low-nibble u in mantissa bits 0..5 -> 1 + u/1024, high-nibble u
+      // in bits 4..9 -> 1 + u/64 (three shifts per word pair)
+      const uint32_t v8 = v >> 8;
+      const uint32_t c1 = c << (4 - c0);           // highs of bytes 0, 2 at bits 4-5 / 8-9 (+16)
+      const uint32_t c18 = c >> (4 + c0);          // highs of bytes 1, 3 at bits 4-5 / 8-9 (+16)
+      const uint32_t p0 = bfi(0x00300030u, c1, bfi(0x000F000Fu, v, magic));
+      const uint32_t p1 = bfi(0x00300030u, c18, bfi(0x000F000Fu, v8, magic));
+      const uint32_t p2 = bfi(0x03000300u, c1, and_or(v, 0x00F000F0u, magic));
+      const uint32_t p3 = bfi(0x03000300u, c18, and_or(v8, 0x00F000F0u, magic));
       const int q = i >> 2;
       S[q] = dot2(p0, xlo[2 * i], S[q]);
       S[q] = dot2(p1, xlo[2 * i + 1], S[q]);
       S[2 + q] = dot2(p2, xhi[2 * i], S[2 + q]);
       S[2 + q] = dot2(p3, xhi[2 * i + 1], S[2 + q]);
     }
-    // sum((u-32) x) = 64 S - 96 X
-    float acc = (float)(int8_t)(r.scl & 0xFF) * (64.f * S[0] - 96.f * xg[0]);
-    acc += (float)(int8_t)(r.scl >> 8) * (64.f * S[1] - 96.f * xg[1]);
+    // sum((u-32) x) = 1024 S - 1056 X (low nibbles), 64 S - 96 X (high nibbles)
+    float acc = (float)(int8_t)(r.scl & 0xFF) * (1024.f * S[0] - 1056.f * xg[0]);
+    acc += (float)(int8_t)(r.scl >> 8) * (1024.f * S[1] - 1056.f * xg[1]);
     acc += (float)(int8_t)(r.sch & 0xFF) * (64.f * S[2] - 96.f * xg[2]);
     acc += (float)(int8_t)(r.sch >> 8) * (64.f * S[3] - 96.f * xg[3]);
     return h2f(r.d) * acc;
