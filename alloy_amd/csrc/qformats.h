@@ -546,24 +546,25 @@ struct FQ50 {
     return r;
   }
   __device__ static float dot(const Raw& r, int, const uint32_t* xp, const float* xg) {
-    const uint32_t qh = r.qh;
-    float S = 0.f;
-    // 5-bit u in fp16 mantissa bits 5..9 -> 1 + u/32; the 5th bits of elements
-    // (l, l+2) are spread to bits 9 and 25 by (t & 5) * 0x00800200.
+    const uint32_t qh = r.qh, magic = MAGIC1;
+    float SA = 0.f, SB = 0.f;
+    // Elements 0..15 (low nibbles): 5-bit u in fp16 mantissa bits 0..4 -> 1 + u/1024;
+    // elements 16..31 (high nibbles): u in bits 4..8 -> 1 + u/64.  The nibbles stay
+    // where they lie (bytes 1, 3 moved down by 8); the 5th bits of four consecutive
+    // elements go to bits 0, 8, 16, 24 by one 24-bit multiply (bit j to bit 8j).
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t v = r.qs[i];
+      const uint32_t v = r.qs[i], v8 = v >> 8;
       const int l = 4 * i;
-      const uint32_t hA0 = (((qh >> l) & 5u) * 0x00800200u) & 0x02000200u;
-      const uint32_t hA1 = (((qh >> (l + 1)) & 5u) * 0x00800200u) & 0x02000200u;
-      const uint32_t hB0 = (((qh >> (l + 16)) & 5u) * 0x00800200u) & 0x02000200u;
-      const uint32_t hB1 = (((qh >> (l + 17)) & 5u) * 0x00800200u) & 0x02000200u;
-      S = dot2(((v << 5) & 0x01E001E0u) | hA0 | MAGIC1, xp[2 * i], S);
-      S = dot2(((v >> 3) & 0x01E001E0u) | hA1 | MAGIC1, xp[2 * i + 1], S);
-      S = dot2(((v << 1) & 0x01E001E0u) | hB0 | MAGIC1, xp[8 + 2 * i], S);
-      S = dot2(((v >> 7) & 0x01E001E0u) | hB1 | MAGIC1, xp[8 + 2 * i + 1], S);
+      const uint32_t sA = (((qh >> l) & 15u) * 0x00204081u) & 0x01010101u;
+      const uint32_t sB = (((qh >> (l + 16)) & 15u) * 0x00204081u) & 0x01010101u;
+      SA = dot2(bfi(0x00100010u, sA << 4, bfi(0x000F000Fu, v, magic)), xp[2 * i], SA);
+      SA = dot2(bfi(0x00100010u, sA >> 4, bfi(0x000F000Fu, v8, magic)), xp[2 * i + 1], SA);
+      SB = dot2(bfi(0x01000100u, sB << 8, and_or(v, 0x00F000F0u, magic)), xp[8 + 2 * i], SB);
+      SB = dot2(bfi(0x01000100u, sB, and_or(v8, 0x00F000F0u, magic)), xp[8 + 2 * i + 1], SB);
     }
-    return h2f(r.d) * (32.f * S - 48.f * (xg[0] + xg[1]));     // sum((u-16) x)
+    // sum((u-16) x) = 1024 SA - 1040 X_A + 64 SB - 80 X_B
+    return h2f(r.d) * (1024.f * SA - 1040.f * xg[0] + (64.f * SB - 80.f * xg[1]));
   }
 };
 
