@@ -412,13 +412,16 @@ struct FQ6K {
 
 // ------------------------------------------------------------------ Q8_0 (wire)
 // 34 B: fp16 d | int8 qs[32]; w = d*q.
+// Sum over 32 int8 weights (words v) of (1 + u/1024) x with u = q + 128: each fp16
+// pair is one byte permute of the offset-binary word with the fp16 1.0 pattern.
+// Callers take sum(q x) = 1024 S - 1152 X.
 __device__ __forceinline__ float q8_words_dot(const uint32_t (&v)[8], const uint32_t* xp, float S) {
   const uint32_t magic = MAGIC1;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const uint32_t o = v[i] ^ 0x80808080u;       // offset binary u = q + 128
-    S = dot2(lshl_or<2>(o & 0x00FF00FFu, magic), xp[2 * i], S);      // bytes 0,2 -> 1 + u/256
-    S = dot2(bfi(0x03FC03FCu, o >> 6, magic), xp[2 * i + 1], S);     // bytes 1,3
+    S = dot2(__builtin_amdgcn_perm(magic, o, 0x07020500u), xp[2 * i], S);       // bytes 0, 2
+    S = dot2(__builtin_amdgcn_perm(magic, o, 0x07030501u), xp[2 * i + 1], S);   // bytes 1, 3
   }
   return S;
 }
@@ -458,7 +461,7 @@ struct FQ80 {
   }
   __device__ static float dot(const Raw& r, int, const uint32_t* xp, const float* xg) {
     const float S = q8_words_dot(r.v, xp, 0.f);
-    return h2f(r.d) * (256.f * S - 384.f * (xg[0] + xg[1]));   // sum((u-128) x)
+    return h2f(r.d) * (1024.f * S - 1152.f * (xg[0] + xg[1]));   // sum((u-128) x)
   }
 };
 
@@ -493,7 +496,7 @@ struct FQ80S {
   }
   __device__ static float dot(const Raw& r, int, const uint32_t* xp, const float* xg) {
     const float S = q8_words_dot(r.v, xp, 0.f);
-    return h2f(r.d) * (256.f * S - 384.f * (xg[0] + xg[1]));
+    return h2f(r.d) * (1024.f * S - 1152.f * (xg[0] + xg[1]));
   }
 };
 
