@@ -79,10 +79,12 @@ typedef enum {
  *   `opts` packs launch knobs for tuning (0 = automatic): bits 0-11 threads per
  *   row of the v_dot2 GEMV (multiple of 16, 16..256), bits 12-27 its grid cap,
  *   bits 28-31 MFMA GEMV row groups, bits 32-35 rows of weights in flight per
- *   thread of the v_dot2 GEMV (2, 3 or 4), bits 36-39 the kernel variant (0
- *   automatic).  GEMV: 1 register ring with an LDS row combine, 2 LDS-staged row
- *   tiles, 3 wave rows with buffer loads and DPP reductions, 4 rows staged through
- *   LDS by aligned 16-byte loads (Q6_K, Q5_0, Q8_0, Q4_K wire blocks).  MFMA GEMV
+ *   thread of the v_dot2 GEMV (2, 3 or 4; for the LDS-staged rows at M = 1: 1 the
+ *   four-row tile, 2 / 4 the tile ring with two / four tiles in flight), bits 36-39
+ *   the kernel variant (0 automatic).  GEMV: 1 register ring with an LDS row
+ *   combine, 2 LDS-staged row tiles, 3 wave rows with buffer loads and DPP
+ *   reductions, 4 rows staged through LDS by aligned 16-byte loads (Q6_K, Q5_0,
+ *   Q8_0, Q4_K wire blocks).  MFMA GEMV
  *   (M <= 16): 1 16x16x32 tiles, 5 Q4_K 4x4x4 broadcast tiles, 6 Q4_K x-stationary
  *   tiles, 7 x-stationary tiles of any format that has them, 8 x-stationary tiles
  *   with the weights dequantised to fp16 before the MFMA (Q4_K, Q6_K, MLX), 9 the
