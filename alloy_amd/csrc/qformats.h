@@ -146,13 +146,14 @@ __device__ __forceinline__ void bwords_a2(__amdgpu_buffer_rsrc_t r, uint32_t off
   for (int i = 0; i < NW; ++i) o[i] = __builtin_amdgcn_alignbyte(t[i + 1], t[i], sh);
 }
 
-// The four fp16 pairs "1 + q/16" of the 8 nibbles of v, in the order
-// (byte0 lo, byte2 lo), (byte1 lo, byte3 lo), (byte0 hi, byte2 hi), (byte1 hi, byte3 hi).
+// The four fp16 pairs "1 + q/1024" of the 8 nibbles of v (each nibble shifted to bits
+// 0-3 of its half), in the order (byte0 lo, byte2 lo), (byte1 lo, byte3 lo),
+// (byte0 hi, byte2 hi), (byte1 hi, byte3 hi).
 __device__ __forceinline__ void nib_pairs(uint32_t v, uint32_t magic, uint32_t (&p)[4]) {
-  p[0] = lshl_or<6>(v & 0x000F000Fu, magic);
-  p[1] = bfi(0x03C003C0u, v >> 2, magic);
-  p[2] = lshl_or<2>(v & 0x00F000F0u, magic);
-  p[3] = bfi(0x03C003C0u, v >> 6, magic);
+  p[0] = bfi(0x000F000Fu, v, magic);
+  p[1] = bfi(0x000F000Fu, v >> 8, magic);
+  p[2] = bfi(0x000F000Fu, v >> 4, magic);
+  p[3] = bfi(0x000F000Fu, v >> 12, magic);
 }
 
 // ------------------------------------------------------------------ Q4_K
@@ -661,7 +662,7 @@ struct FMLX {
       S = dot2(pr[2], xp[4 * i + 2], S);
       S = dot2(pr[3], xp[4 * i + 3], S);
     }
-    const float s16 = 16.f * h2f(r.s);
-    return s16 * S + (h2f(r.b) - s16) * (xg[0] + xg[1]);           // s sum(q x) + b X
+    const float s1k = 1024.f * h2f(r.s);
+    return s1k * S + (h2f(r.b) - s1k) * (xg[0] + xg[1]);           // s sum(q x) + b X
   }
 };
