@@ -365,7 +365,7 @@ struct XsQ6KW {
     r.sh = sh * 8u;                                // as a bit shift
   }
   __device__ static uint32_t al(uint32_t hi, uint32_t lo, uint32_t shb) {
-    return (uint32_t)(((uint64_t)hi << 32 | lo) >> shb);
+    return __builtin_amdgcn_alignbit(hi, lo, shb);      // (hi:lo) >> shb, shb < 32
   }
   // slot S: elements 128 (kq / 2) + 32 (kq % 2 + 2 (S / 4)) + 8 (S % 4) .. + 7
   __device__ static f16x8 xload(__amdgpu_buffer_rsrc_t xr, uint32_t off, int S, int kq) {
@@ -390,7 +390,9 @@ struct XsQ6KW {
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const uint32_t v = al(r.ql[wq + k + 1], r.ql[wq + k], shb), u = al(r.qh[wq + k + 1], r.qh[wq + k], shb);
-      const uint32_t q4 = ((v >> (4 * hi)) & 0x0F0F0F0Fu) | (((u >> qsh) & 0x03030303u) << 4);
+      // u rotated right by qsh - 4: each byte's 2-bit field lands at its bits 4-5
+      const uint32_t ur = __builtin_amdgcn_alignbit(u, u, (qsh + 28u) & 31u);
+      const uint32_t q4 = bfi(0x30303030u, ur, (v >> (4 * hi)) & 0x0F0F0F0Fu);
       b[2 * k] = xs_dq2(__builtin_amdgcn_perm(0u, q4, 0x0c010c00u), sm, c);
       b[2 * k + 1] = xs_dq2(__builtin_amdgcn_perm(0u, q4, 0x0c030c02u), sm, c);
     }
