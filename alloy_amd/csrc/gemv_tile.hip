@@ -129,11 +129,11 @@ __global__ __launch_bounds__(256) void k_gemv_t(const uint8_t* w, int64_t rbytes
 
 // M = 1 over long rows: R = 1, 2 or 4 rows per tile so that the tile's units cover
 // at least 192 of the 256 threads (thread t takes row t / (256 / R) and every
-// (256 / R)-th unit of it), D tiles in flight in registers (ring slot = tile mod D), two LDS tile buffers
-// and one barrier per tile.  Tiles stay within 16 KiB where k_gemv_t's four rows
-// would pass its 48 KiB (Q8_0 rows of 14336 elements and longer).  Each wave's sum
-// goes to LDS; the tile's rows are completed and stored after the next tile's
-// barrier (the thread of row r sums its row's waves).
+// (256 / R)-th unit of it), D tiles in flight in registers (ring slot = tile mod D),
+// two LDS tile buffers and one barrier per tile.  Tiles stay within 16 KiB where
+// k_gemv_t's four rows would pass its 48 KiB (Q8_0 rows of 14336 elements and
+// longer).  Each wave's sum goes to LDS; the tile's rows are completed and stored
+// after the next tile's barrier (the thread of row r sums its row's waves).
 template <class F, typename YT, int D, int CPL>
 __global__ __launch_bounds__(256) void k_gemv_rt(const uint8_t* w, int64_t rbytes, int Kx, const f16* x, YT* y,
                                                  int N, int R, int ntiles) {
