@@ -303,30 +303,6 @@ struct XsQ6K {
     s = h2f(r.d) * (float)(int8_t)((r.scw[C >> 2] >> (8 * (C & 3))) & 0xFFu);
     c = -1056.f * s;                              // (q - 32) with q stored as 1024 + q
   }
-  // the 6-bit values of chain C, one per byte (elements 4 kq .. + 3 of group C)
-  template <int C>
-  __device__ static uint32_t q6(const Raw& r) {
-    constexpr int S = C >> 1, g2 = C & 1, h = S >> 2, s = S & 3;
-    const uint32_t ql = r.ql[4 * h + 2 * (s & 1) + g2], qh = r.qh[2 * h + g2];
-    return ((ql >> (4 * (s >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * s)) & 0x03030303u) << 4);
-  }
-  // chains C - 1 and C (odd C: the two halves of slot C / 2) with the weights
-  // dequantised to fp16 (d sc (q - 32), rounded once), one 16x16x32 MFMA
-  template <int C>
-  __device__ static void dq(const f16x8* xu, const Raw& r, f32x4& acc) {
-    if constexpr (C & 1) {
-      const float d = h2f(r.d);
-      const float sa = d * (float)(int8_t)((r.scw[(C - 1) >> 2] >> (8 * ((C - 1) & 3))) & 0xFFu);
-      const float sb = d * (float)(int8_t)((r.scw[C >> 2] >> (8 * (C & 3))) & 0xFFu);
-      const uint32_t va = q6<C - 1>(r), vb = q6<C>(r);
-      const float ma = sa * 16777216.f, mb = sb * 16777216.f, ca = -32.f * sa, cb = -32.f * sb;
-      const u32x4 b = {xs_dq2(__builtin_amdgcn_perm(0u, va, 0x0c010c00u), ma, ca),
-                       xs_dq2(__builtin_amdgcn_perm(0u, va, 0x0c030c02u), ma, ca),
-                       xs_dq2(__builtin_amdgcn_perm(0u, vb, 0x0c010c00u), mb, cb),
-                       xs_dq2(__builtin_amdgcn_perm(0u, vb, 0x0c030c02u), mb, cb)};
-      acc = xs_mfma32(xu[C >> 1], b, acc);
-    }
-  }
 };
 
 // Q6_K with the weights dequantised to fp16 (d sc (q - 32), rounded once), read as
