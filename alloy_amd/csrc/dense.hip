@@ -1208,8 +1208,10 @@ hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, 
   }
   // few activation rows on few rows: the LDS-staged v_dot2 kernel (weights read once,
   // decoded once per row and token) beats the MFMA kernels' fixed cost — measured on
-  // the BASELINE decode shapes at M = 2, 3, 4, 8
-  const bool tile_small_m = fmt == F_Q6_K || fmt == F_Q5_0 || fmt == F_Q8_0 ? M * N <= 3072
+  // the BASELINE decode shapes at M = 2, 3, 4, 8 and K = 4096 at M = 2..8 on 512-2048
+  // rows (Q6_K 4096 x 1024 M = 4: 5.9 against 7.1 us; M = 6: 7.5 against 7.1)
+  const bool tile_small_m = fmt == F_Q6_K || fmt == F_Q5_0 || fmt == F_Q8_0
+                                ? M * N <= 3072 || (M <= 4 && M * N <= 4096)
                           : fmt == F_Q4_K && M == 2 && (N <= 1024 || a.K >= 8192);
   const int v = o.variant ? o.variant : tile_small_m ? 9 : mfma_variant(fmt, M, N, a.K);
   hipError_t e = hipErrorNotSupported;
