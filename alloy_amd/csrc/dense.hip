@@ -1196,12 +1196,13 @@ hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, 
   if (splits > 1 && (!ws || ws_bytes < (int64_t)splits * M * N * 4 || (M * N) % 4 || ((uintptr_t)ws & 15) ||
                      ((uintptr_t)y & (y_f32 ? 15 : 7))))
     splits = 1;
-  // Q4_K and MLX, few activation rows on few rows (M <= 8, M N <= 6144): the v_dot2
-  // wave-row kernel (16-byte aligned units, each decoded once and dotted with every
-  // token) beats the MFMA kernels' fixed cost — Q4_K 3072 x 1024 at M = 2 / 4 / 6:
-  // 2.9 / 3.9 / 4.8 us against 4.0 / 5.1 / 5.3 us, 8192 x 1024 M = 4 6.4 against 10.5;
-  // at M N = 8192 the MFMA kernels win (M = 4, 3072 x 2048: 5.2 against 6.2)
-  if (o.variant == 0 && (fmt == F_Q4_K || fmt == F_MLX) && M <= 8 && M * N <= 6144) {
+  // Q4_K, MLX and split Q8_0, few activation rows on few rows (M <= 8, M N <= 6144):
+  // the v_dot2 wave-row kernel (16-byte aligned units, each decoded once and dotted
+  // with every token) beats the MFMA kernels' fixed cost — Q4_K 3072 x 1024 at
+  // M = 2 / 4 / 6: 2.9 / 3.9 / 4.8 us against 4.0 / 5.1 / 5.3 us, 8192 x 1024 M = 4 6.4
+  // against 10.5; split Q8_0 4096 x 1024 M = 4 3.9 against 7.0; at M N = 8192 the MFMA
+  // kernels win (Q4_K M = 4, 3072 x 2048: 5.2 against 6.2)
+  if (o.variant == 0 && (fmt == F_Q4_K || fmt == F_MLX || fmt == F_Q8_0S) && M <= 8 && M * N <= 6144) {
     const hipError_t e = launch_gemv_dot2(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
     if (e != hipErrorNotSupported) return e;
     (void)hipGetLastError();
