@@ -1174,8 +1174,15 @@ static int mfma_variant(int fmt, int64_t M, int64_t N, int64_t K) {
 // 4096x2048 10.7 -> 9.5 us); at 192 tiles and more splits lose (extra partial traffic
 // and the summing launch).  K >= 4096 keeps at least four units per split; Q4_K over
 // K = 8192 takes the Q4_K x-stationary kernel, which does not split.
+// Q4_K, MLX and split Q8_0 with few activation rows on few rows run the v_dot2
+// wave-row kernel at M <= 16 (launch_gemv_mfma), which takes no workspace
+static bool dot2_small_m(int fmt, int64_t M, int64_t N) {
+  return (fmt == F_Q4_K || fmt == F_MLX || fmt == F_Q8_0S) && M <= 8 && M * N <= 6144;
+}
+
 static int gemv_splits(int fmt, int64_t M, int64_t N, int64_t K) {
   if (M < 8 || M > 16 || K < 4096 || K % 256 || (fmt == F_Q4_K && K > 8192)) return 1;
+  if (dot2_small_m(fmt, M, N)) return 1;
   if (fmt != F_Q4_K && fmt != F_Q6_K && fmt != F_Q5_0 && fmt != F_Q8_0 && fmt != F_Q8_0S && fmt != F_MLX) return 1;
   const int64_t tiles = (N + 15) / 16;
   return tiles <= 64 ? 4 : tiles <= 128 ? 2 : 1;
@@ -1202,7 +1209,7 @@ hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, 
   // M = 2 / 4 / 6: 2.9 / 3.9 / 4.8 us against 4.0 / 5.1 / 5.3 us, 8192 x 1024 M = 4 6.4
   // against 10.5; split Q8_0 4096 x 1024 M = 4 3.9 against 7.0; at M N = 8192 the MFMA
   // kernels win (Q4_K M = 4, 3072 x 2048: 5.2 against 6.2)
-  if (o.variant == 0 && (fmt == F_Q4_K || fmt == F_MLX || fmt == F_Q8_0S) && M <= 8 && M * N <= 6144) {
+  if (o.variant == 0 && dot2_small_m(fmt, M, N)) {
     const hipError_t e = launch_gemv_dot2(fmt, a, x, x_f32, y, y_f32, M, N, o, st);
     if (e != hipErrorNotSupported) return e;
     (void)hipGetLastError();

@@ -79,6 +79,9 @@ def test_split_workspace_plan():
     assert lib.alloy_gemm_workspace_bytes(F["q6_k"], 8, 1024, 3072) == 0
     assert lib.alloy_gemm_workspace_bytes(F["q4_k"], 16, 1024, 11008) == 0
     assert lib.alloy_gemm_workspace_bytes(F["q4_k"], 1, 1024, 4096) == 0
+    # few rows and tokens: the v_dot2 wave-row kernel, no split
+    assert lib.alloy_gemm_workspace_bytes(F["q4_k"], 8, 512, 4096) == 0
+    assert lib.alloy_gemm_workspace_bytes(F["q6_k"], 8, 512, 4096) == 4 * 8 * 512 * 4
 
 
 def meta(shape, dtype):
