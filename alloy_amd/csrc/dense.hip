@@ -1175,8 +1175,12 @@ static int mfma_variant(int fmt, int64_t M, int64_t N, int64_t K) {
 // and the summing launch).  K >= 4096 keeps at least four units per split; Q4_K over
 // K = 8192 takes the Q4_K x-stationary kernel, which does not split.
 // Q4_K, MLX and split Q8_0 with few activation rows on few rows run the v_dot2
-// wave-row kernel at M <= 16 (launch_gemv_mfma), which takes no workspace
+// wave-row kernel at M <= 16 (launch_gemv_mfma), which takes no workspace; split
+// Q5_0, whose M <= 16 alternative is the generic 16x16x32 kernel, up to M N = 12288
+// and at M = 2 on any N (4096 x 14336: 19.0 against 22.7 us; M = 4 4096 x 4096:
+// 12.7 against 12.4)
 static bool dot2_small_m(int fmt, int64_t M, int64_t N) {
+  if (fmt == F_Q5_0S) return M <= 8 && (M <= 2 || M * N <= 12288);
   return (fmt == F_Q4_K || fmt == F_MLX || fmt == F_Q8_0S) && M <= 8 && M * N <= 6144;
 }
 
