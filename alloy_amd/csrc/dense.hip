@@ -1079,6 +1079,10 @@ static hipError_t launch_xs_job(int fmt, XsJob j, const Opts& o, hipStream_t st,
       j.sb = (uint32_t)(a.K / 16);               // fp16 scales per row
       return launch_xs<XsDQ<XsQ80S>, 0>(j, 0, dcap, rt, st);
     }
+    if (fmt == F_Q5_0S) {
+      j.sb = (uint32_t)(a.K / 16);
+      return launch_xs<XsDQ<XsQ50S>, 0>(j, 0, dcap, rt, st);
+    }
   } else {
     if (fmt == F_Q4_K) return launch_xs<XsQ4K, 0>(j, 0, cap, o.row_groups, st);
     if (fmt == F_Q6_K) return launch_xs<XsQ6K, 0>(j, 0, cap, o.row_groups, st);
@@ -1152,7 +1156,7 @@ hipError_t launch_glu_combine(int act, const float* g, const float* u, void* y, 
 //   Q4_K  tall (N >= 32768) and 3 <= M <= 6: 4x4x4 broadcast kernel; K <= 8192: the
 //         x-stationary kernel with fp16-dequantised weights (8); else the Q4_K
 //         x-stationary kernel
-//   Q6_K, Q5_0, Q8_0 (wire blocks) and split Q8_0  x-stationary with fp16-dequantised
+//   Q6_K, Q5_0, Q8_0 (wire blocks), split Q8_0 / Q5_0  x-stationary with fp16-dequantised
 //         weights (K over 4096: in passes over K)
 //   MLX   generic x-stationary (exact products); N >= 12288: the dequantising
 //         provider with 16-byte loads, one workgroup per CU looping over the tiles
@@ -1162,7 +1166,7 @@ static int mfma_variant(int fmt, int64_t M, int64_t N, int64_t K) {
     if (N >= 32768 && M >= 3 && M <= 6) return 5;
     return K <= 8192 ? 8 : 6;
   }
-  if (fmt == F_Q6_K || fmt == F_Q5_0 || fmt == F_Q8_0 || fmt == F_Q8_0S) return 8;
+  if (fmt == F_Q6_K || fmt == F_Q5_0 || fmt == F_Q8_0 || fmt == F_Q8_0S || fmt == F_Q5_0S) return 8;
   if (fmt == F_MLX) return N >= 12288 ? 8 : 7;
   return 1;
 }
@@ -1174,20 +1178,20 @@ static int mfma_variant(int fmt, int64_t M, int64_t N, int64_t K) {
 // 4096x2048 10.7 -> 9.5 us); at 192 tiles and more splits lose (extra partial traffic
 // and the summing launch).  K >= 4096 keeps at least four units per split; Q4_K over
 // K = 8192 takes the Q4_K x-stationary kernel, which does not split.
-// Q4_K, MLX and split Q8_0 with few activation rows on few rows run the v_dot2
-// wave-row kernel at M <= 16 (launch_gemv_mfma), which takes no workspace; split
-// Q5_0, whose M <= 16 alternative is the generic 16x16x32 kernel, up to M N = 12288
-// and at M = 2 on any N (4096 x 14336: 19.0 against 22.7 us; M = 4 4096 x 4096:
-// 12.7 against 12.4)
+// Q4_K, MLX and the split layouts with few activation rows on few rows run the v_dot2
+// wave-row kernel at M <= 16 (launch_gemv_mfma), which takes no workspace (split
+// Q5_0 4096 x 1024 M = 4: 4.5 against 7.0 us on its x-stationary provider; 4096 x
+// 4096 M = 2: 8.7 against 7.3)
 static bool dot2_small_m(int fmt, int64_t M, int64_t N) {
-  if (fmt == F_Q5_0S) return M <= 8 && (M <= 2 || M * N <= 12288);
-  return (fmt == F_Q4_K || fmt == F_MLX || fmt == F_Q8_0S) && M <= 8 && M * N <= 6144;
+  return (fmt == F_Q4_K || fmt == F_MLX || fmt == F_Q8_0S || fmt == F_Q5_0S) && M <= 8 && M * N <= 6144;
 }
 
 static int gemv_splits(int fmt, int64_t M, int64_t N, int64_t K) {
   if (M < 8 || M > 16 || K < 4096 || K % 256 || (fmt == F_Q4_K && K > 8192)) return 1;
   if (dot2_small_m(fmt, M, N)) return 1;
-  if (fmt != F_Q4_K && fmt != F_Q6_K && fmt != F_Q5_0 && fmt != F_Q8_0 && fmt != F_Q8_0S && fmt != F_MLX) return 1;
+  if (fmt != F_Q4_K && fmt != F_Q6_K && fmt != F_Q5_0 && fmt != F_Q8_0 && fmt != F_Q8_0S && fmt != F_Q5_0S &&
+      fmt != F_MLX)
+    return 1;
   const int64_t tiles = (N + 15) / 16;
   return tiles <= 64 ? 4 : tiles <= 128 ? 2 : 1;
 }
@@ -1207,7 +1211,7 @@ hipError_t launch_gemv_mfma(int fmt, const QArgs& a, const void* x, bool x_f32, 
   if (splits > 1 && (!ws || ws_bytes < (int64_t)splits * M * N * 4 || (M * N) % 4 || ((uintptr_t)ws & 15) ||
                      ((uintptr_t)y & (y_f32 ? 15 : 7))))
     splits = 1;
-  // Q4_K, MLX and split Q8_0, few activation rows on few rows (M <= 8, M N <= 6144):
+  // Q4_K, MLX and split Q8_0 / Q5_0, few activation rows on few rows (M <= 8, M N <= 6144):
   // the v_dot2 wave-row kernel (16-byte aligned units, each decoded once and dotted
   // with every token) beats the MFMA kernels' fixed cost — Q4_K 3072 x 1024 at
   // M = 2 / 4 / 6: 2.9 / 3.9 / 4.8 us against 4.0 / 5.1 / 5.3 us, 8192 x 1024 M = 4 6.4

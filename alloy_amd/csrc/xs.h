@@ -492,6 +492,48 @@ struct XsQ80S {
   }
 };
 
+// Q5_0 in the split layout (qweight u8[N, K/2] K-sequential nibbles, qhigh u8[N, K/2]
+// with element k's 5th bit at bit 0 and element k + 1's at bit 4 of byte k / 2, fp16
+// scales [N, K/32]): lane kq of a 256-element unit takes its 64 contiguous elements
+// (two 16-byte loads each of qweight and qhigh) and its two blocks' scales (one
+// dword).  Chain C is slot C: elements 64 kq + 8 C .. + 7 in natural order, from
+// word C of each array; the even elements' 5-bit values are formed in the bytes of
+// one word, the odd ones' in another, and one byte permute per pair interleaves
+// them into the fp16 halves (denormal integers), dequantised as d (u - 16).
+struct XsQ50S {
+  static constexpr int NCH = 8;
+  static constexpr bool WIDE = false;
+  struct Raw { uint32_t q[8], h[8]; uint32_t d; };
+  __device__ static void load(const Src& src, uint32_t rw, uint32_t rs, int unit, int kq, Raw& r) {
+    const uint32_t bo = rw + (uint32_t)unit * 128u + 32u * (uint32_t)kq;
+    const u32x4 q0 = bld16(src.w, bo), q1 = bld16(src.w, bo + 16u);
+    const u32x4 h0 = bld16(src.aux, bo), h1 = bld16(src.aux, bo + 16u);
+    r.q[0] = q0.x; r.q[1] = q0.y; r.q[2] = q0.z; r.q[3] = q0.w;
+    r.q[4] = q1.x; r.q[5] = q1.y; r.q[6] = q1.z; r.q[7] = q1.w;
+    r.h[0] = h0.x; r.h[1] = h0.y; r.h[2] = h0.z; r.h[3] = h0.w;
+    r.h[4] = h1.x; r.h[5] = h1.y; r.h[6] = h1.z; r.h[7] = h1.w;
+    r.d = bld4(src.s, rs + (uint32_t)unit * 16u + 4u * (uint32_t)kq);
+  }
+  __device__ static f16x8 xload(__amdgpu_buffer_rsrc_t xr, uint32_t off, int S, int kq) {
+    return xs_x8(xr, off + 2u * (uint32_t)(64 * kq + 8 * S));
+  }
+  template <int C>
+  __device__ static void dq(const f16x8* xu, const Raw& r, f32x4& acc) {
+    constexpr int blk = C >> 2;
+    const float dd = h2f(blk ? r.d >> 16 : r.d), s = dd * 16777216.f, c = -16.f * dd;
+    const uint32_t q = r.q[C], h = r.h[C];
+    // byte j: even element 2j (low nibble, 5th bit at bit 0), odd element 2j + 1 (high
+    // nibble, 5th bit at bit 4)
+    const uint32_t ev = bfi(0x0F0F0F0Fu, q, (h & 0x01010101u) << 4);
+    const uint32_t od = bfi(0x0F0F0F0Fu, q >> 4, h & 0x10101010u);
+    uint32_t b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)   // halves (element 2j, element 2j + 1)
+      b[j] = xs_dq2(__builtin_amdgcn_perm(od, ev, 0x0c000c00u | (uint32_t)j | ((uint32_t)(4 + j) << 16)), s, c);
+    acc = xs_mfma32(xu[C], u32x4{b[0], b[1], b[2], b[3]}, acc);
+  }
+};
+
 // MLX 4-bit affine with the weights dequantised to fp16 (s q + b, rounded once), any
 // group size 32 << GSH: every lane reads two 16-byte runs of four words (words 4 kq
 // .. + 3 and 16 + 4 kq .. + 3 of the unit; MFMA S takes word 16 (S / 4) + 4 kq + S % 4),

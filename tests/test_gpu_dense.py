@@ -176,17 +176,18 @@ def test_gemv_mfma(dev, fmt, M):
     for rg in (1, 2):
         y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=rg << 28).cpu().numpy()
         check(y, x, wt.W, f"{fmt} gemv_mfma M={M} rg={rg}")
-    if fmt in ("q4_k", "q6_k", "mlx_q4", "q8_0", "q5_0", "q8_0_split") and M <= 16:
+    if fmt in ("q4_k", "q6_k", "mlx_q4", "q8_0", "q5_0", "q8_0_split", "q5_0_split") and M <= 16:
         # every kernel explicitly: 1 = 16x16x32 tiles, 5 = 4x4x4 broadcast (Q4_K),
         # 6 = x-stationary 16x16x32 (Q4_K), 7 = generic x-stationary (Q4_K, Q6_K, MLX),
         # 8 = x-stationary with fp16-dequantised weights (Q4_K, Q6_K, MLX, Q8_0, Q5_0)
-        variants = {"q4_k": (1, 5, 6, 7, 8), "q8_0": (1, 8), "q5_0": (1, 8), "q8_0_split": (1, 8)}.get(fmt, (1, 7, 8))
+        variants = {"q4_k": (1, 5, 6, 7, 8), "q8_0": (1, 8), "q5_0": (1, 8), "q8_0_split": (1, 8),
+                    "q5_0_split": (1, 8)}.get(fmt, (1, 7, 8))
         for variant in variants:
             y = wt.qmm(xt, path="gemv_mfma", out_dtype=torch.float32, opts=variant << 36).cpu().numpy()
             check(y, x, wt.W, f"{fmt} gemv_mfma M={M} variant={variant}")
 
 
-@pytest.mark.parametrize("fmt", ["q6_k", "q5_0", "q8_0", "q8_0_split"])
+@pytest.mark.parametrize("fmt", ["q6_k", "q5_0", "q8_0", "q8_0_split", "q5_0_split"])
 @pytest.mark.parametrize("M", [3, 8, 16])
 @pytest.mark.parametrize("K,N", [(8192, 72), (11008, 33), (14336, 40)])
 def test_gemv_xs_multipass(dev, fmt, M, K, N):
@@ -204,7 +205,7 @@ def test_gemv_xs_multipass(dev, fmt, M, K, N):
     check(y16, x, wt.W, f"{fmt} xs multi-pass fp16 out M={M} K={K} N={N}")
 
 
-@pytest.mark.parametrize("fmt", ["q4_k", "q6_k", "q5_0", "q8_0", "q8_0_split", "mlx_q4"])
+@pytest.mark.parametrize("fmt", ["q4_k", "q6_k", "q5_0", "q8_0", "q8_0_split", "q5_0_split", "mlx_q4"])
 @pytest.mark.parametrize("M", [3, 8, 16])
 @pytest.mark.parametrize("K,N,splits", [(2048, 132, 3), (8192, 72, 2), (8192, 72, 5), (11008, 40, 4),
                                         (1024, 40, 7), (2048, 130, 2)])
