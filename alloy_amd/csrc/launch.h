@@ -73,8 +73,8 @@ hipError_t launch_gemm(int fmt, const QArgs& a, const void* x, bool x_f32, void*
 int64_t gemm_workspace_bytes(int fmt, int64_t M, int64_t N, int64_t K);
 
 // Gated pair y = act(x G^T) * (x U^T) (act 0 silu, 1 gelu in tanh form): one fused
-// launch for M <= 16 when glu_fused_supported(), else two products into fp32
-// buffers and launch_glu_combine over them.
+// launch when glu_fused_supported() (Q4_K / MLX, M <= 16, the shapes where it is
+// faster), else two products into fp32 buffers and launch_glu_combine over them.
 bool glu_fused_supported(int fmt, int64_t M, int64_t N, int64_t K, bool x_f32, int gs);
 hipError_t launch_glu_fused(int fmt, int act, const QArgs& g, const QArgs& u, const void* x, bool x_f32,
                             void* y, bool y_f32, int64_t M, int64_t N, const Opts& o, hipStream_t st);

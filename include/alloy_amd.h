@@ -234,10 +234,11 @@ alloy_status alloy_qmm_batched(alloy_format fmt, int32_t n, const void* const* w
  * format (each passed like alloy_qmm's w / aux / scales / biases) — the reference's
  * *_silu / *_gelu ops (custom_ops.py:53-58, 79-82, 108-111; kernels
  * packages/alloy-metal/src/alloy/std/quant.py:356-759, 1456-1940, 2833-2887).
- * For M <= 16 (Q4_K, MLX with a power-of-two group size <= 256, K % 256 == 0,
- * K <= 4096, fp16 x) one launch reads both matrices and applies the activation in
- * its epilogue and no workspace is needed; otherwise the two products go to fp32
- * workspace buffers and a combine kernel writes y.  workspace: >=
+ * With K % 256 == 0, K <= 4096 and fp16 x, for Q4_K at 4 <= M <= 16 and N <= 4096 and
+ * for MLX (power-of-two group size <= 256) at M == 1 or M <= 16 and N <= 4096, one
+ * launch reads both matrices and applies the activation in its epilogue and no
+ * workspace is needed; otherwise the two products go to fp32 workspace buffers and a
+ * combine kernel writes y.  workspace: >=
  * alloy_glu_workspace_bytes(...) bytes, 256-byte aligned (may be NULL when that is 0).
  */
 size_t alloy_glu_workspace_bytes(alloy_format fmt, int64_t M, int64_t N, int64_t K, int32_t group_size,

@@ -1,7 +1,7 @@
 """GPU parity of the fused gated pair y = act(x G^T) * (x U^T) (the reference's
 gguf_q4_k_silu / gguf_q4_k_gelu / mlx_q4_silu / gguf_q8_0_silu ops) against the
-NumPy oracle, through the C ABI: the one-launch x-stationary path (M <= 16) and the
-two-product + combine path (larger M, other formats)."""
+NumPy oracle, through the C ABI: the one-launch x-stationary path (Q4_K / MLX at
+M <= 16 where it is the faster one) and the two-product + combine path (the rest)."""
 
 import numpy as np
 import pytest
@@ -43,7 +43,7 @@ def check_glu(y, x, G, U, act, what):
 
 @pytest.mark.parametrize("fmt", ["q4_k", "mlx_q4", "q8_0_split", "q6_k"])
 @pytest.mark.parametrize("act", ["silu", "gelu"])
-@pytest.mark.parametrize("M", [1, 3, 16, 40])
+@pytest.mark.parametrize("M", [1, 3, 4, 16, 40])
 def test_glu_matches_oracle(dev, fmt, act, M):
     rng = np.random.default_rng(M * 7 + len(fmt))
     N, K = 200, 2048
@@ -80,14 +80,15 @@ def test_named_glu_ops(dev, M):
     assert torch.equal(y, alloy_amd.qmm_glu("q8_0_split", "silu", x, g8, u8))
 
 
-def test_glu_decode_shape_fused(dev):
-    # Llama-3.2-3B gate/up at decode: K = 3072, N = 8192, M = 1 and 4 (one launch)
+@pytest.mark.parametrize("N,K,Ms", [(8192, 3072, (1, 4)), (4096, 4096, (4, 9, 16))])
+def test_glu_decode_shapes(dev, N, K, Ms):
+    # Llama-3.2-3B gate/up at decode (K = 3072, N = 8192: two products + combine) and a
+    # 4096 x 4096 pair at M = 4..16 (one fused launch)
     rng = np.random.default_rng(5)
-    N, K = 8192, 3072
     gate, G = make("q4_k", N, K, rng, dev)
     up, U = make("q4_k", N, K, rng, dev)
-    for M in (1, 4):
+    for M in Ms:
         x = synth.numpy_x(M, K, rng)
         y = alloy_amd.qmm_glu("q4_k", "silu", torch.from_numpy(x).to(dev), gate, up, out_dtype=torch.float32)
         rows = rng.choice(N, 64, replace=False)
-        check_glu(y.cpu().numpy()[:, rows], x, G[rows], U[rows], "silu", f"decode gate/up M={M}")
+        check_glu(y.cpu().numpy()[:, rows], x, G[rows], U[rows], "silu", f"decode gate/up {N}x{K} M={M}")
