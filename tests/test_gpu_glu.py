@@ -80,10 +80,10 @@ def test_named_glu_ops(dev, M):
     assert torch.equal(y, alloy_amd.qmm_glu("q8_0_split", "silu", x, g8, u8))
 
 
-@pytest.mark.parametrize("N,K,Ms", [(8192, 3072, (1, 4)), (4096, 4096, (4, 9, 16))])
+@pytest.mark.parametrize("N,K,Ms", [(8192, 3072, (1, 4)), (4096, 4096, (2, 4, 9, 16))])
 def test_glu_decode_shapes(dev, N, K, Ms):
     # Llama-3.2-3B gate/up at decode (K = 3072, N = 8192: two products + combine) and a
-    # 4096 x 4096 pair at M = 4..16 (one fused launch)
+    # 4096 x 4096 pair at M = 2..16 (one fused launch)
     rng = np.random.default_rng(5)
     gate, G = make("q4_k", N, K, rng, dev)
     up, U = make("q4_k", N, K, rng, dev)
