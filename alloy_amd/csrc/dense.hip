@@ -1109,13 +1109,15 @@ static hipError_t launch_xs_job(int fmt, XsJob j, const Opts& o, hipStream_t st,
 bool glu_fused_supported(int fmt, int64_t M, int64_t N, int64_t K, bool x_f32, int gs) {
   if (x_f32 || M < 1 || M > 16 || K % 256 || K > 4096 || N >= (1ll << 31)) return false;
   // Fused only where it wins (us per pair, fused against two products + combine).
-  // Q4_K: loses wherever the products take the v_dot2 GEMVs (M = 1: K 3072 N 8192
-  // 25.7 / 12.3, K 2048 N 768 7.1 / 6.3; M = 2, N 768: 7.3 / 6.8), wins up to N = 4096
-  // against the MFMA GEMVs (K 4096 N 4096 M = 2: 12.4 / 16.2) and loses past it (K 3072
-  // N 8192 M = 16: 27.2 / 21.3).  MLX: M = 1 wins at every N (12.7 / 13.0, 6.4 / 7.3);
-  // M >= 2 loses past N = 4096 (M = 2: 24.7 / 19.1, M = 4: 26.5 / 20.1).
-  if (fmt == F_Q4_K) return N <= 4096 && (M >= 4 || M * N > 6144);
-  return fmt == F_MLX && gs >= 32 && gs <= 256 && !(gs & (gs - 1)) && (M == 1 || N <= 4096);
+  // Q4_K loses wherever the products take the v_dot2 GEMVs (M = 1: K 3072 N 8192
+  // 15.8 / 12.3, K 2048 N 768 7.1 / 6.3; M = 2, N 768: 7.3 / 6.8) and wins against the
+  // MFMA GEMVs (K 4096 N 4096 M = 2: 12.3 / 16.2; K 3072 N 8192 M = 16: 20.0 / 21.1).
+  // MLX wins at M = 1 (12.6 / 13.0, 6.4 / 7.3) and M >= 2 (K 3072 N 8192 M = 4: 16.5 /
+  // 20.3).  Past N = 8192 both lose (K 4096 N 14336 M = 4: Q4_K 45.2 / 36.1, MLX 43.2 /
+  // 36.3).
+  if (N > 8192) return false;
+  if (fmt == F_Q4_K) return M >= 4 || (M >= 2 && M * N > 6144);
+  return fmt == F_MLX && gs >= 32 && gs <= 256 && !(gs & (gs - 1));
 }
 
 hipError_t launch_glu_fused(int fmt, int act, const QArgs& g, const QArgs& u, const void* x, bool x_f32,

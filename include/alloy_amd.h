@@ -234,8 +234,8 @@ alloy_status alloy_qmm_batched(alloy_format fmt, int32_t n, const void* const* w
  * format (each passed like alloy_qmm's w / aux / scales / biases) — the reference's
  * *_silu / *_gelu ops (custom_ops.py:53-58, 79-82, 108-111; kernels
  * packages/alloy-metal/src/alloy/std/quant.py:356-759, 1456-1940, 2833-2887).
- * With K % 256 == 0, K <= 4096 and fp16 x, for Q4_K at M <= 16, N <= 4096 and M >= 4
- * or M * N > 6144, and for MLX (power-of-two group size <= 256) at M == 1 or M <= 16 and N <= 4096, one
+ * With K % 256 == 0, K <= 4096, N <= 8192 and fp16 x, for Q4_K at 4 <= M <= 16 or
+ * M >= 2 and M * N > 6144, and for MLX (power-of-two group size <= 256) at M <= 16, one
  * launch reads both matrices and applies the activation in its epilogue and no
  * workspace is needed; otherwise the two products go to fp32 workspace buffers and a
  * combine kernel writes y.  workspace: >=

@@ -80,15 +80,19 @@ def test_named_glu_ops(dev, M):
     assert torch.equal(y, alloy_amd.qmm_glu("q8_0_split", "silu", x, g8, u8))
 
 
-@pytest.mark.parametrize("N,K,Ms", [(8192, 3072, (1, 4)), (4096, 4096, (2, 4, 9, 16))])
-def test_glu_decode_shapes(dev, N, K, Ms):
-    # Llama-3.2-3B gate/up at decode (K = 3072, N = 8192: two products + combine) and a
-    # 4096 x 4096 pair at M = 2..16 (one fused launch)
+@pytest.mark.parametrize("fmt,N,K,Ms", [("q4_k", 8192, 3072, (1, 4)), ("q4_k", 4096, 4096, (2, 4, 9, 16)),
+                                         ("mlx_q4", 8192, 3072, (1, 2, 16)), ("q4_k", 8320, 2048, (3, 16))])
+def test_glu_decode_shapes(dev, fmt, N, K, Ms):
+    # Llama-3.2-3B gate/up at decode (K = 3072, N = 8192: two products + combine for
+    # Q4_K at M = 1, one fused launch otherwise), a 4096 x 4096 pair at M = 2..16
+    # (fused) and N = 8320 (past the fused limit: two products + combine)
     rng = np.random.default_rng(5)
-    gate, G = make("q4_k", N, K, rng, dev)
-    up, U = make("q4_k", N, K, rng, dev)
+    gs = 64 if fmt == "mlx_q4" else 0
+    gate, G = make(fmt, N, K, rng, dev)
+    up, U = make(fmt, N, K, rng, dev)
     for M in Ms:
         x = synth.numpy_x(M, K, rng)
-        y = alloy_amd.qmm_glu("q4_k", "silu", torch.from_numpy(x).to(dev), gate, up, out_dtype=torch.float32)
+        y = alloy_amd.qmm_glu(fmt, "silu", torch.from_numpy(x).to(dev), gate, up, group_size=gs,
+                              out_dtype=torch.float32)
         rows = rng.choice(N, 64, replace=False)
-        check_glu(y.cpu().numpy()[:, rows], x, G[rows], U[rows], "silu", f"decode gate/up {N}x{K} M={M}")
+        check_glu(y.cpu().numpy()[:, rows], x, G[rows], U[rows], "silu", f"{fmt} gate/up {N}x{K} M={M}")

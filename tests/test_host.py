@@ -85,9 +85,9 @@ def test_split_workspace_plan():
 
 
 def test_glu_workspace_plan():
-    """The gated pair runs as one fused launch (no workspace) for Q4_K at M <= 16,
-    N <= 4096 and M >= 4 or M * N > 6144, and for MLX at M = 1 or M <= 16 and N <= 4096; every other case
-    takes two fp32 product buffers."""
+    """The gated pair runs as one fused launch (no workspace) at N <= 8192 and M <= 16
+    for Q4_K at M >= 4 or M >= 2 with M * N > 6144 and for MLX at any such M; every
+    other case takes two fp32 product buffers."""
     lib = alloy_amd.lib()
     F = _lib.FMT
     assert lib.alloy_glu_workspace_bytes(F["q4_k"], 4, 1024, 4096, 0, _lib.DT_F16) == 0
@@ -95,11 +95,14 @@ def test_glu_workspace_plan():
     assert lib.alloy_glu_workspace_bytes(F["q4_k"], 1, 1024, 4096, 0, _lib.DT_F16) == 2 * 1024 * 4
     assert lib.alloy_glu_workspace_bytes(F["q4_k"], 2, 4096, 4096, 0, _lib.DT_F16) == 0
     assert lib.alloy_glu_workspace_bytes(F["q4_k"], 2, 768, 2048, 0, _lib.DT_F16) == 2 * 2 * 768 * 4
-    assert lib.alloy_glu_workspace_bytes(F["q4_k"], 4, 8192, 3072, 0, _lib.DT_F16) == 2 * 4 * 8192 * 4
+    assert lib.alloy_glu_workspace_bytes(F["q4_k"], 4, 8192, 3072, 0, _lib.DT_F16) == 0
+    assert lib.alloy_glu_workspace_bytes(F["q4_k"], 4, 14336, 4096, 0, _lib.DT_F16) == 2 * 4 * 14336 * 4
+    assert lib.alloy_glu_workspace_bytes(F["q4_k"], 1, 8192, 3072, 0, _lib.DT_F16) == 2 * 8192 * 4
     assert lib.alloy_glu_workspace_bytes(F["q4_k"], 17, 1024, 4096, 0, _lib.DT_F16) == 2 * 17 * 1024 * 4
     assert lib.alloy_glu_workspace_bytes(F["q6_k"], 8, 1024, 4096, 0, _lib.DT_F16) == 2 * 8 * 1024 * 4
     assert lib.alloy_glu_workspace_bytes(F["mlx_q4"], 1, 8192, 3072, 64, _lib.DT_F16) == 0
-    assert lib.alloy_glu_workspace_bytes(F["mlx_q4"], 4, 8192, 3072, 64, _lib.DT_F16) == 2 * 4 * 8192 * 4
+    assert lib.alloy_glu_workspace_bytes(F["mlx_q4"], 4, 8192, 3072, 64, _lib.DT_F16) == 0
+    assert lib.alloy_glu_workspace_bytes(F["mlx_q4"], 1, 14336, 4096, 64, _lib.DT_F16) == 2 * 14336 * 4
 
 
 def meta(shape, dtype):
